@@ -1,0 +1,293 @@
+// kvq_capi.cpp -- the extern "C" surface of libkvq.so (declared in include/kvq.h).
+//
+// Every entry point validates its arguments before making any HIP call, so the
+// error paths (null pointers, bad shapes, undersized workspace) are testable on
+// a machine without a GPU, as in kv_cache/KV_int8_split_optimized.cu:272-273.
+#include <limits.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <algorithm>
+#include <mutex>
+
+#include "../../include/kvq.h"
+#include "kvq_internal.hpp"
+
+namespace {
+
+using kvq::DecodeArgs;
+using kvq::DecodePlan;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr size_t kAlign = 256;
+// Workgroups a decode launch aims for when it picks the split count itself:
+// 8 per CU on MI355X's 256 CUs.
+constexpr int kTargetWorkgroups = 2048;
+
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Split count and workspace layout for one decode problem.
+// max_splits bounds the splits (scratch capacity of the reference ABI);
+// fused selects the arrival-counter merge (workspace holds counters).
+DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, int requested,
+                     int max_splits, bool fused) {
+    DecodePlan p{};
+    const int G = Hq / Hkv;
+    const int tile = kvq::fast_tile_tokens(d);
+    p.fast = tile > 0 && aligned;
+    p.sg = p.fast ? kvq::fast_heads_per_group(G) : 1;
+    p.nsg = p.fast ? G / p.sg : G;
+    const long units = p.fast ? static_cast<long>(B) * Hkv * p.nsg : static_cast<long>(B) * Hq;
+    const int gran = p.fast ? tile : 64;
+    max_len = std::max(max_len, 1);
+    long splits;
+    int chunk;
+    if (requested > 0) {
+        splits = std::min<long>(requested, max_len);
+        splits = std::min<long>(splits, std::max(max_splits, 1));
+        chunk = static_cast<int>((max_len + splits - 1) / splits);
+    } else {
+        splits = (kTargetWorkgroups + units - 1) / units;
+        splits = std::min<long>(splits, (max_len + gran - 1) / gran);
+        splits = std::max<long>(1, std::min<long>(splits, std::max(max_splits, 1)));
+        chunk = static_cast<int>((max_len + splits - 1) / splits);
+        if (splits > 1) chunk = static_cast<int>(round_up(static_cast<size_t>(chunk), gran));
+    }
+    p.chunk = chunk;
+    p.splits = (max_len + chunk - 1) / chunk;
+    if (p.splits > 1) {
+        const size_t recs = static_cast<size_t>(B) * Hq * p.splits;
+        p.counter_bytes = (fused && p.fast) ? round_up(sizeof(int) * static_cast<size_t>(units), kAlign) : 0;
+        p.ml_bytes = round_up(recs * 2 * sizeof(float), kAlign);
+        p.acc_bytes = round_up(recs * static_cast<size_t>(d) * sizeof(float), kAlign);
+    }
+    return p;
+}
+
+size_t plan_bytes(const DecodePlan& p) { return p.counter_bytes + p.ml_bytes + p.acc_bytes; }
+
+void bind_workspace(DecodeArgs& a, const DecodePlan& p, void* ws) {
+    char* base = static_cast<char*>(ws);
+    a.counters = p.counter_bytes ? reinterpret_cast<int*>(base) : nullptr;
+    a.part_ml = p.splits > 1 ? reinterpret_cast<float*>(base + p.counter_bytes) : nullptr;
+    a.part_acc = p.splits > 1 ? reinterpret_cast<float*>(base + p.counter_bytes + p.ml_bytes) : nullptr;
+}
+
+bool shape_ok(int H, int N, int d) { return H > 0 && N > 0 && d > 0 && d <= KVQ_MAX_HEAD_DIM; }
+
+// Reference-ABI problem ([H,N,d], one query per head) as a batched problem.
+DecodeArgs reference_args(const float* Q, const int8_t* K, const int8_t* V, const float* ks,
+                          const float* vs, float* out, int H, int N, int d) {
+    DecodeArgs a{};
+    a.q = Q;
+    a.k = const_cast<int8_t*>(K);
+    a.v = const_cast<int8_t*>(V);
+    a.ks = const_cast<float*>(ks);
+    a.vs = const_cast<float*>(vs);
+    a.out = out;
+    a.B = 1;
+    a.Hq = a.Hkv = H;
+    a.G = 1;
+    a.cap = N;
+    a.d = d;
+    a.uniform_len = N;
+    a.max_len = N;
+    a.scale_log2 = (1.0f / sqrtf(static_cast<float>(d))) * kLog2e;
+    return a;
+}
+
+bool reference_aligned(const float* Q, const int8_t* K, const int8_t* V, int d) {
+    return aligned16(Q) && aligned16(K) && aligned16(V) && (d % 16) == 0;
+}
+
+hipError_t reference_launch(const float* Q, const int8_t* K, const int8_t* V, const float* ks,
+                            const float* vs, float* out, int H, int N, int d, float* S,
+                            hipStream_t stream) {
+    if (!Q || !K || !V || !ks || !vs || !out || !S || !shape_ok(H, N, d)) return hipErrorInvalidValue;
+    if (static_cast<long long>(H) * N > INT_MAX) return hipErrorInvalidValue;
+    DecodeArgs a = reference_args(Q, K, V, ks, vs, out, H, N, d);
+    // S holds H*N floats; a split needs (d + 2) floats per head.
+    const int max_splits = std::max(1, N / (d + 2));
+    const DecodePlan p = make_plan(1, H, H, d, N, reference_aligned(Q, K, V, d), 0, max_splits, false);
+    a.splits = p.splits;
+    a.chunk = p.chunk;
+    a.nsg = p.nsg;
+    bind_workspace(a, p, S);
+    return kvq::launch_decode(a, p, stream);
+}
+
+// Library-owned, per-device split workspace for the legacy `solve` ABI.  Grown
+// on demand (hipFree waits for in-flight work) and zero-filled on allocation;
+// completed launches leave the arrival counters at zero.
+struct SolveWorkspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+SolveWorkspace g_ws[64];
+
+hipError_t solve_workspace(size_t need, void** out) {
+    *out = nullptr;
+    if (need == 0) return hipSuccess;
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    SolveWorkspace& w = g_ws[dev];
+    if (w.bytes < need) {
+        if (w.ptr) {
+            err = hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.bytes = 0;
+            if (err != hipSuccess) return err;
+        }
+        const size_t bytes = round_up(need, 1 << 20);
+        err = hipMalloc(&w.ptr, bytes);
+        if (err != hipSuccess) return err;
+        err = kvq::launch_fill_zero(w.ptr, bytes, nullptr);
+        if (err != hipSuccess) return err;
+        w.bytes = bytes;
+    }
+    *out = w.ptr;
+    return hipSuccess;
+}
+
+bool decode_params_ok(const kvq_decode_params* p) {
+    if (!p) return false;
+    if (p->batch <= 0 || p->num_q_heads <= 0 || p->num_kv_heads <= 0) return false;
+    if (p->num_q_heads % p->num_kv_heads != 0) return false;
+    if (p->head_dim <= 0 || p->head_dim > KVQ_MAX_HEAD_DIM || p->capacity <= 0) return false;
+    if (p->max_seq_len < 0 || p->num_splits < 0) return false;
+    if (!p->lengths && p->max_seq_len == 0) return false;
+    if (p->max_seq_len > p->capacity) return false;
+    if (!p->q || !p->k_cache || !p->v_cache || !p->k_scale || !p->v_scale || !p->out) return false;
+    if ((p->k_new == nullptr) != (p->v_new == nullptr)) return false;
+    const long long units = static_cast<long long>(p->batch) * p->num_q_heads;
+    if (units > INT_MAX / 4) return false;
+    return true;
+}
+
+int decode_max_len(const kvq_decode_params* p) { return p->max_seq_len > 0 ? p->max_seq_len : p->capacity; }
+
+bool decode_aligned(const kvq_decode_params* p) {
+    return aligned16(p->q) && aligned16(p->k_cache) && aligned16(p->v_cache) && (p->head_dim % 16) == 0 &&
+           (!p->k_new || (aligned16(p->k_new) && aligned16(p->v_new)));
+}
+
+DecodePlan decode_plan(const kvq_decode_params* p) {
+    return make_plan(p->batch, p->num_q_heads, p->num_kv_heads, p->head_dim, decode_max_len(p),
+                     decode_aligned(p), p->num_splits, INT_MAX, true);
+}
+
+}  // namespace
+
+extern "C" {
+
+void solve(const float* Q, const int8_t* K_int8, const int8_t* V_int8, const float* k_scale,
+           const float* v_scale, float* output, int num_heads, int seq_len, int head_dim) {
+    if (!Q || !K_int8 || !V_int8 || !k_scale || !v_scale || !output) {
+        fprintf(stderr, "[kvq] solve: null pointer input: Q=%p K_int8=%p V_int8=%p k_scale=%p v_scale=%p output=%p\n",
+                static_cast<const void*>(Q), static_cast<const void*>(K_int8), static_cast<const void*>(V_int8),
+                static_cast<const void*>(k_scale), static_cast<const void*>(v_scale), static_cast<void*>(output));
+        return;
+    }
+    if (!shape_ok(num_heads, seq_len, head_dim) || static_cast<long long>(num_heads) * seq_len > INT_MAX) {
+        fprintf(stderr, "[kvq] solve: invalid shape: num_heads=%d, seq_len=%d, head_dim=%d (head_dim <= %d)\n",
+                num_heads, seq_len, head_dim, KVQ_MAX_HEAD_DIM);
+        return;
+    }
+    DecodeArgs a = reference_args(Q, K_int8, V_int8, k_scale, v_scale, output, num_heads, seq_len, head_dim);
+    const DecodePlan p = make_plan(1, num_heads, num_heads, head_dim, seq_len,
+                                   reference_aligned(Q, K_int8, V_int8, head_dim), 0, INT_MAX, true);
+    a.splits = p.splits;
+    a.chunk = p.chunk;
+    a.nsg = p.nsg;
+    void* ws = nullptr;
+    hipError_t err = solve_workspace(plan_bytes(p), &ws);
+    if (err == hipSuccess) {
+        bind_workspace(a, p, ws);
+        err = kvq::launch_decode(a, p, nullptr);
+    }
+    if (err != hipSuccess) fprintf(stderr, "[kvq] solve: HIP error: %s (%s)\n", hipGetErrorName(err), hipGetErrorString(err));
+}
+
+hipError_t kv_int8_split_launch(const float* Q, const int8_t* K_int8, const int8_t* V_int8,
+                                const float* k_scale, const float* v_scale, float* output,
+                                int num_heads, int seq_len, int head_dim, float* S, hipStream_t stream) {
+    return reference_launch(Q, K_int8, V_int8, k_scale, v_scale, output, num_heads, seq_len, head_dim, S, stream);
+}
+
+hipError_t kv_int8_simple_launch(const float* Q, const int8_t* K_int8, const int8_t* V_int8,
+                                 const float* k_scale, const float* v_scale, float* output,
+                                 int num_heads, int seq_len, int head_dim, float* S, hipStream_t stream) {
+    return reference_launch(Q, K_int8, V_int8, k_scale, v_scale, output, num_heads, seq_len, head_dim, S, stream);
+}
+
+size_t kvq_decode_workspace_size(const kvq_decode_params* p) {
+    if (!decode_params_ok(p)) return 0;
+    return plan_bytes(decode_plan(p));
+}
+
+hipError_t kvq_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (workspace_bytes == 0) return hipSuccess;
+    if (!workspace) return hipErrorInvalidValue;
+    return kvq::launch_fill_zero(workspace, workspace_bytes, stream);
+}
+
+hipError_t kvq_decode_launch(const kvq_decode_params* p, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
+    if (!decode_params_ok(p)) return hipErrorInvalidValue;
+    const DecodePlan plan = decode_plan(p);
+    const size_t need = plan_bytes(plan);
+    if (need > 0 && (!workspace || workspace_bytes < need)) return hipErrorInvalidValue;
+    DecodeArgs a{};
+    a.q = p->q;
+    a.k = p->k_cache;
+    a.v = p->v_cache;
+    a.ks = p->k_scale;
+    a.vs = p->v_scale;
+    a.out = p->out;
+    a.lengths = p->lengths;
+    a.k_new = p->k_new;
+    a.v_new = p->v_new;
+    a.B = p->batch;
+    a.Hq = p->num_q_heads;
+    a.Hkv = p->num_kv_heads;
+    a.G = p->num_q_heads / p->num_kv_heads;
+    a.cap = p->capacity;
+    a.d = p->head_dim;
+    a.uniform_len = decode_max_len(p);
+    a.max_len = decode_max_len(p);
+    a.splits = plan.splits;
+    a.chunk = plan.chunk;
+    a.nsg = plan.nsg;
+    const float scale = p->softmax_scale > 0.0f ? p->softmax_scale : 1.0f / sqrtf(static_cast<float>(p->head_dim));
+    a.scale_log2 = scale * kLog2e;
+    bind_workspace(a, plan, workspace);
+    return kvq::launch_decode(a, plan, stream);
+}
+
+hipError_t kvq_append_launch(const kvq_append_params* p, hipStream_t stream) {
+    if (!p || p->batch <= 0 || p->num_kv_heads <= 0 || p->head_dim <= 0 || p->head_dim > KVQ_MAX_HEAD_DIM ||
+        p->capacity <= 0 || !p->k_new || !p->v_new || !p->k_cache || !p->v_cache || !p->k_scale || !p->v_scale)
+        return hipErrorInvalidValue;
+    if (static_cast<long long>(p->batch) * p->num_kv_heads > INT_MAX) return hipErrorInvalidValue;
+    return kvq::launch_append(p->k_new, p->v_new, p->k_cache, p->v_cache, p->k_scale, p->v_scale, p->positions,
+                              p->uniform_position, false, p->batch, p->num_kv_heads, p->capacity,
+                              p->capacity, p->head_dim, stream);
+}
+
+hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, int8_t* q, float* scale,
+                                    hipStream_t stream) {
+    if (rows < 0 || head_dim <= 0 || head_dim > KVQ_MAX_HEAD_DIM) return hipErrorInvalidValue;
+    if (rows > 0 && (!x || !q || !scale)) return hipErrorInvalidValue;
+    return kvq::launch_quantize_rows(x, rows, head_dim, q, scale, stream);
+}
+
+const char* kvq_version(void) { return "kvq 0.1.0 gfx950"; }
+
+}  // extern "C"

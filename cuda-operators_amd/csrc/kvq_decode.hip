@@ -1,0 +1,470 @@
+// kvq_decode.hip -- gfx950 decode-attention kernels over an int8 K/V cache.
+//
+// Math (per query head, the reference's cpu_reference,
+// kv_cache/KV_int8_split_optimized.cu:385-437): s_t = (q . K_t) * k_scale_t *
+// softmax_scale, p = softmax(s), out = sum_t p_t * V_t * v_scale_t.  Scores are
+// kept in log2 units (softmax_scale * log2 e folded into one multiplier) so
+// every exponential is one v_exp_f32.
+//
+// decode_fast<D, SG>: one workgroup (4 waves) per (sequence split, batch,
+//   kv head, group of SG query heads).  A token's D-byte K row is read by D/16
+//   lanes with one 16-byte load each, so one wave load covers 64*16 contiguous
+//   bytes (several whole rows).  Each lane dequantises its 16 bytes in
+//   registers (SDWA sign-extended byte converts), forms 16-element partial dots
+//   for its SG query heads and finishes them with DPP row sums over the token's
+//   lane group.  Every lane group keeps its own online-softmax state (max, sum,
+//   16 accumulators per head) with no cross-lane traffic per token; states are
+//   merged across lane groups (ds_bpermute), then across waves (LDS), once per
+//   workgroup.  Each K/V byte is read once per kv head: the SG query heads of a
+//   group share the loads.
+//   A sequence longer than one chunk is split; each split writes a partial
+//   (max, sum, acc[D]) record, and the last split to finish (device-scope
+//   arrival counter) merges the records with a log-sum-exp reduction, so the
+//   whole decode is a single kernel.  Without counters (caller scratch of
+//   unknown contents) merge_kernel does the merge instead.
+//   Optionally the workgroup owning a sequence's last token first quantises that
+//   token from fp32 (append) and attends to it from registers.
+//
+// decode_generic: any head dim up to KVQ_MAX_HEAD_DIM and any alignment; one
+//   wave per (split, batch, query head), q and the accumulators in LDS.  It is
+//   the correctness path for shapes the tuned kernel does not cover.
+#include <math.h>
+
+#include "kvq_device.hpp"
+#include "kvq_internal.hpp"
+
+namespace kvq {
+namespace {
+
+constexpr int kFastWaves = 4;  // waves per workgroup
+constexpr int kFastU = 4;      // tokens per lane group per loop iteration
+
+template <int D>
+struct FastGeom {
+    static constexpr int LPT = D / 16;          // lanes per token
+    static constexpr int TPL = kWave / LPT;     // tokens per wave load
+    static constexpr int WSTEP = TPL * kFastU;  // tokens per wave iteration
+    static constexpr int BSTEP = WSTEP * kFastWaves;
+};
+
+__device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
+    const int len = a.lengths ? a.lengths[b] : a.uniform_len;
+    return min(max(len, 0), a.max_len);
+}
+
+// Log-sum-exp merge of the nsplit partial records of output row bhq, element dim.
+__device__ float merge_dim(const DecodeArgs& a, size_t bhq, int dim, int nsplit) {
+    const float* ml = a.part_ml + bhq * a.splits * 2;
+    const float* acc = a.part_acc + bhq * a.splits * a.d;
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, ml[2 * s]);
+    float L = 0.0f, A = 0.0f;
+    for (int s = 0; s < nsplit; s++) {
+        const float w = fast_exp2(ml[2 * s] - M);
+        L = fmaf(ml[2 * s + 1], w, L);
+        A = fmaf(acc[static_cast<size_t>(s) * a.d + dim], w, A);
+    }
+    return A / L;
+}
+
+// Online-softmax update of one lane group's state with U tokens (one per load).
+template <int SG, int U, int LPT>
+__device__ __forceinline__ void attend(const float (&qr)[SG][16], const int4 (&kk)[U],
+                                       const int4 (&vv)[U], const float (&kscl)[U],
+                                       const float (&vscl)[U], const bool (&ok)[U],
+                                       float scale_log2, float (&m)[SG], float (&l)[SG],
+                                       float (&acc)[SG][16]) {
+    float s[SG][U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        float kf[16];
+        unpack16(kk[u], kf);
+#pragma unroll
+        for (int h = 0; h < SG; h++) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; j++) dot = fmaf(qr[h][j], kf[j], dot);
+            dot = group_sum<LPT>(dot);
+            s[h][u] = ok[u] ? (dot * kscl[u]) * scale_log2 : -INFINITY;
+        }
+    }
+    float w[SG][U];
+#pragma unroll
+    for (int h = 0; h < SG; h++) {
+        float mx = m[h];
+#pragma unroll
+        for (int u = 0; u < U; u++) mx = fmaxf(mx, s[h][u]);
+        const float ms = (mx == -INFINITY) ? 0.0f : mx;
+        const float alpha = fast_exp2(m[h] - ms);
+        l[h] *= alpha;
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc[h][j] *= alpha;
+        m[h] = mx;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const float p = fast_exp2(s[h][u] - ms);
+            l[h] += p;
+            w[h][u] = p * vscl[u];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        float vf[16];
+        unpack16(vv[u], vf);
+#pragma unroll
+        for (int h = 0; h < SG; h++) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) acc[h][j] = fmaf(w[h][u], vf[j], acc[h][j]);
+        }
+    }
+}
+
+template <int D, int SG>
+__global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArgs a) {
+    using Geo = FastGeom<D>;
+    constexpr int LPT = Geo::LPT;
+    constexpr int TPL = Geo::TPL;
+    constexpr int U = kFastU;
+    __shared__ float s_ml[kFastWaves][SG][2];
+    __shared__ float s_acc[kFastWaves][SG][D];
+    __shared__ int s_last;
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int tg = lane / LPT;  // token slot within a wave load
+    const int ds = lane % LPT;  // 16-element slice of the head dim
+
+    const int units = a.B * a.Hkv * a.nsg;
+    const int split = blockIdx.x / units;
+    const int unit = blockIdx.x - split * units;
+    const int bh = unit / a.nsg;
+    const int sgi = unit - bh * a.nsg;
+    const int b = bh / a.Hkv;
+    const int kvh = bh - b * a.Hkv;
+    const int hq0 = kvh * a.G + sgi * SG;
+    const size_t bhq0 = static_cast<size_t>(b) * a.Hq + hq0;
+    const int len = seq_len_of(a, b);
+    const int nsplit = (len + a.chunk - 1) / a.chunk;
+
+    if (len == 0) {
+        if (split == 0)
+            for (int i = threadIdx.x; i < SG * D; i += blockDim.x) a.out[bhq0 * D + i] = 0.0f;
+        return;
+    }
+    if (split >= nsplit) return;
+
+    const int t0 = split * a.chunk;
+    const int t1 = min(len, t0 + a.chunk);
+    const bool app = (a.k_new != nullptr) && (t1 == len);
+    const int tend = app ? t1 - 1 : t1;  // tokens read from the cache
+
+    float qr[SG][16];
+#pragma unroll
+    for (int h = 0; h < SG; h++) {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + (bhq0 + h) * D + ds * 16);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 x = qp[j];
+            qr[h][4 * j + 0] = x.x;
+            qr[h][4 * j + 1] = x.y;
+            qr[h][4 * j + 2] = x.z;
+            qr[h][4 * j + 3] = x.w;
+        }
+    }
+    float m[SG], l[SG], acc[SG][16];
+#pragma unroll
+    for (int h = 0; h < SG; h++) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc[h][j] = 0.0f;
+    }
+
+    const size_t row0 = static_cast<size_t>(bh) * a.cap;
+    const int8_t* kp = a.k + row0 * D + ds * 16;
+    const int8_t* vp = a.v + row0 * D + ds * 16;
+    const float* ksp = a.ks + row0;
+    const float* vsp = a.vs + row0;
+
+    for (int base = t0 + wave * Geo::WSTEP; base < tend; base += Geo::BSTEP) {
+        int4 kk[U], vv[U];
+        float kscl[U], vscl[U];
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int t = base + u * TPL + tg;
+            ok[u] = t < tend;
+            const int tc = ok[u] ? t : tend - 1;
+            kk[u] = *reinterpret_cast<const int4*>(kp + static_cast<size_t>(tc) * D);
+            vv[u] = *reinterpret_cast<const int4*>(vp + static_cast<size_t>(tc) * D);
+            kscl[u] = ksp[tc];
+            vscl[u] = vsp[tc];
+        }
+        attend<SG, U, LPT>(qr, kk, vv, kscl, vscl, ok, a.scale_log2, m, l, acc);
+    }
+
+    if (app && wave == 0) {
+        // Quantise the appended token (same rule and bits as append_kernel),
+        // store it once per kv head, and attend to it from registers.
+        const float4* kn = reinterpret_cast<const float4*>(a.k_new + static_cast<size_t>(bh) * D + ds * 16);
+        const float4* vn = reinterpret_cast<const float4*>(a.v_new + static_cast<size_t>(bh) * D + ds * 16);
+        float xk[16], xv[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 x = kn[j], y = vn[j];
+            xk[4 * j] = x.x; xk[4 * j + 1] = x.y; xk[4 * j + 2] = x.z; xk[4 * j + 3] = x.w;
+            xv[4 * j] = y.x; xv[4 * j + 1] = y.y; xv[4 * j + 2] = y.z; xv[4 * j + 3] = y.w;
+        }
+        float ak = 0.0f, av = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            ak = fmaxf(ak, fabsf(xk[j]));
+            av = fmaxf(av, fabsf(xv[j]));
+        }
+        ak = group_max<LPT>(ak);
+        av = group_max<LPT>(av);
+        const float sk = quant_scale(ak), sv = quant_scale(av);
+        int qk[16], qv[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            qk[j] = quant_one(xk[j], sk);
+            qv[j] = quant_one(xv[j], sv);
+        }
+        int4 kk1[1], vv1[1];
+        kk1[0] = make_int4(pack4(qk[0], qk[1], qk[2], qk[3]), pack4(qk[4], qk[5], qk[6], qk[7]),
+                           pack4(qk[8], qk[9], qk[10], qk[11]), pack4(qk[12], qk[13], qk[14], qk[15]));
+        vv1[0] = make_int4(pack4(qv[0], qv[1], qv[2], qv[3]), pack4(qv[4], qv[5], qv[6], qv[7]),
+                           pack4(qv[8], qv[9], qv[10], qv[11]), pack4(qv[12], qv[13], qv[14], qv[15]));
+        const int tnew = len - 1;
+        if (sgi == 0 && tg == 0) {
+            *reinterpret_cast<int4*>(a.k + (row0 + tnew) * D + ds * 16) = kk1[0];
+            *reinterpret_cast<int4*>(a.v + (row0 + tnew) * D + ds * 16) = vv1[0];
+            if (ds == 0) {
+                a.ks[row0 + tnew] = sk;
+                a.vs[row0 + tnew] = sv;
+            }
+        }
+        const float sk1[1] = {sk}, sv1[1] = {sv};
+        const bool ok1[1] = {tg == 0};
+        attend<SG, 1, LPT>(qr, kk1, vv1, sk1, sv1, ok1, a.scale_log2, m, l, acc);
+    }
+
+    // Merge the lane groups of this wave (lanes that share ds).
+#pragma unroll
+    for (int off = LPT; off < kWave; off <<= 1) {
+#pragma unroll
+        for (int h = 0; h < SG; h++) {
+            const float mo = __shfl_xor(m[h], off);
+            const float lo = __shfl_xor(l[h], off);
+            const float mx = fmaxf(m[h], mo);
+            const float ms = (mx == -INFINITY) ? 0.0f : mx;
+            const float a1 = fast_exp2(m[h] - ms), a2 = fast_exp2(mo - ms);
+            l[h] = l[h] * a1 + lo * a2;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const float ao = __shfl_xor(acc[h][j], off);
+                acc[h][j] = acc[h][j] * a1 + ao * a2;
+            }
+            m[h] = mx;
+        }
+    }
+    if (tg == 0) {
+#pragma unroll
+        for (int h = 0; h < SG; h++) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) s_acc[wave][h][ds * 16 + j] = acc[h][j];
+            if (ds == 0) {
+                s_ml[wave][h][0] = m[h];
+                s_ml[wave][h][1] = l[h];
+            }
+        }
+    }
+    __syncthreads();
+
+    // Merge the waves; one thread per (head, element).
+    for (int i = threadIdx.x; i < SG * D; i += blockDim.x) {
+        const int h = i / D;
+        const int dim = i - h * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kFastWaves; w++) M = fmaxf(M, s_ml[w][h][0]);
+        const float Ms = (M == -INFINITY) ? 0.0f : M;
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kFastWaves; w++) {
+            const float f = fast_exp2(s_ml[w][h][0] - Ms);
+            L = fmaf(s_ml[w][h][1], f, L);
+            A = fmaf(s_acc[w][h][dim], f, A);
+        }
+        if (nsplit == 1) {
+            a.out[(bhq0 + h) * D + dim] = A / L;
+        } else {
+            const size_t rec = (bhq0 + h) * a.splits + split;
+            a.part_acc[rec * D + dim] = A;
+            if (dim == 0) {
+                a.part_ml[rec * 2] = M;
+                a.part_ml[rec * 2 + 1] = L;
+            }
+        }
+    }
+
+    if (nsplit > 1 && a.counters != nullptr) {
+        // Release this split's record, count arrivals; the last arrival merges.
+        __threadfence();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int prev = atomicAdd(a.counters + unit, 1);
+            s_last = (prev == nsplit - 1);
+        }
+        __syncthreads();
+        if (s_last) {
+            __threadfence();
+            for (int i = threadIdx.x; i < SG * D; i += blockDim.x) {
+                const int h = i / D;
+                const int dim = i - h * D;
+                a.out[(bhq0 + h) * D + dim] = merge_dim(a, bhq0 + h, dim, nsplit);
+            }
+            if (threadIdx.x == 0) a.counters[unit] = 0;  // ready for the next launch
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a) {
+    const int bhq = blockIdx.x;
+    const int b = bhq / a.Hq;
+    const int len = seq_len_of(a, b);
+    const int nsplit = (len + a.chunk - 1) / a.chunk;
+    if (nsplit <= 1) return;  // written directly by the decode kernel
+    for (int dim = threadIdx.x; dim < a.d; dim += blockDim.x)
+        a.out[static_cast<size_t>(bhq) * a.d + dim] = merge_dim(a, bhq, dim, nsplit);
+}
+
+__global__ __launch_bounds__(kWave) void decode_generic(const DecodeArgs a) {
+    extern __shared__ float sh[];
+    float* qs = sh;
+    float* accs = sh + a.d;
+    const int lane = threadIdx.x;
+    const int bhqn = a.B * a.Hq;
+    const int split = blockIdx.x / bhqn;
+    const int bhq = blockIdx.x - split * bhqn;
+    const int b = bhq / a.Hq;
+    const int hq = bhq - b * a.Hq;
+    const int kvh = hq / a.G;
+    const int d = a.d;
+    const int len = seq_len_of(a, b);
+    const int nsplit = (len + a.chunk - 1) / a.chunk;
+    float* outp = a.out + static_cast<size_t>(bhq) * d;
+    if (len == 0) {
+        if (split == 0)
+            for (int i = lane; i < d; i += kWave) outp[i] = 0.0f;
+        return;
+    }
+    if (split >= nsplit) return;
+    const int t0 = split * a.chunk;
+    const int t1 = min(len, t0 + a.chunk);
+    const size_t row0 = (static_cast<size_t>(b) * a.Hkv + kvh) * a.cap;
+
+    for (int i = lane; i < d; i += kWave) {
+        qs[i] = a.q[static_cast<size_t>(bhq) * d + i];
+        accs[i] = 0.0f;
+    }
+    __syncthreads();
+
+    float m = -INFINITY, l = 0.0f;
+    for (int t = t0; t < t1; t++) {
+        const int8_t* kr = a.k + (row0 + t) * d;
+        const int8_t* vr = a.v + (row0 + t) * d;
+        float dot = 0.0f;
+        for (int i = lane; i < d; i += kWave) dot = fmaf(qs[i], static_cast<float>(kr[i]), dot);
+        dot = wave_sum(dot);
+        const float s = (dot * a.ks[row0 + t]) * a.scale_log2;
+        const float mx = fmaxf(m, s);
+        const float alpha = fast_exp2(m - mx);
+        const float p = fast_exp2(s - mx);
+        l = l * alpha + p;
+        const float w = p * a.vs[row0 + t];
+        for (int i = lane; i < d; i += kWave) accs[i] = fmaf(w, static_cast<float>(vr[i]), accs[i] * alpha);
+        m = mx;
+    }
+    if (nsplit == 1) {
+        for (int i = lane; i < d; i += kWave) outp[i] = accs[i] / l;
+    } else {
+        const size_t rec = static_cast<size_t>(bhq) * a.splits + split;
+        for (int i = lane; i < d; i += kWave) a.part_acc[rec * d + i] = accs[i];
+        if (lane == 0) {
+            a.part_ml[rec * 2] = m;
+            a.part_ml[rec * 2 + 1] = l;
+        }
+    }
+}
+
+template <int D>
+hipError_t launch_fast_d(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(a.B * a.Hkv * p.nsg * p.splits));
+    const dim3 block(kFastWaves * kWave);
+    switch (p.sg) {
+        case 1: hipLaunchKernelGGL((decode_fast<D, 1>), grid, block, 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((decode_fast<D, 2>), grid, block, 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((decode_fast<D, 4>), grid, block, 0, stream, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int fast_tile_tokens(int d) {
+    switch (d) {
+        case 32: return FastGeom<32>::BSTEP;
+        case 64: return FastGeom<64>::BSTEP;
+        case 128: return FastGeom<128>::BSTEP;
+        case 256: return FastGeom<256>::BSTEP;
+        default: return 0;
+    }
+}
+
+int fast_heads_per_group(int G) {
+    if (G % 4 == 0) return 4;
+    if (G % 2 == 0) return 2;
+    return 1;
+}
+
+hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(merge_kernel, dim3(static_cast<unsigned>(a.B * a.Hq)), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
+    hipError_t err;
+    if (p.fast) {
+        switch (a.d) {
+            case 32: err = launch_fast_d<32>(a, p, stream); break;
+            case 64: err = launch_fast_d<64>(a, p, stream); break;
+            case 128: err = launch_fast_d<128>(a, p, stream); break;
+            case 256: err = launch_fast_d<256>(a, p, stream); break;
+            default: return hipErrorInvalidValue;
+        }
+        if (err != hipSuccess) return err;
+        if (a.counters == nullptr && p.splits > 1) return launch_merge(a, stream);
+        return hipSuccess;
+    }
+    DecodeArgs g = a;
+    if (a.k_new != nullptr) {
+        // Generic path: append first (token length-1 of each sequence), then attend.
+        err = launch_append(a.k_new, a.v_new, a.k, a.v, a.ks, a.vs, a.lengths,
+                            min(max(a.uniform_len, 0), a.max_len) - 1, true, a.B, a.Hkv, a.max_len,
+                            a.cap, a.d, stream);
+        if (err != hipSuccess) return err;
+        g.k_new = g.v_new = nullptr;
+    }
+    g.counters = nullptr;
+    const dim3 grid(static_cast<unsigned>(a.B * a.Hq * p.splits));
+    const size_t lds = sizeof(float) * 2 * static_cast<size_t>(a.d);
+    hipLaunchKernelGGL(decode_generic, grid, dim3(kWave), lds, stream, g);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    if (p.splits > 1) return launch_merge(g, stream);
+    return hipSuccess;
+}
+
+}  // namespace kvq

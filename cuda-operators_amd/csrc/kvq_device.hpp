@@ -1,0 +1,99 @@
+// kvq_device.hpp -- device helpers shared by the gfx950 kernels of libkvq.so.
+//
+// Wave64 throughout.  Cross-lane sums inside a token's lane group use DPP row
+// permutations (no LDS traffic); wider exchanges use ds_bpermute (__shfl_xor).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvq {
+
+constexpr int kWave = 64;
+
+// DPP control words (GCN/CDNA DPP encoding).
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141; // lane i <- 7-i within each 8 lanes
+constexpr int kDppRowMirror = 0x140;     // lane i <- 15-i within each 16 lanes
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of N lanes (N in {1,2,4,8,16}); every lane of the
+// group receives the group total.  After the two quad steps each quad holds its
+// sum, so a half-row mirror adds the neighbouring quad and a row mirror adds
+// the other half of the 16-lane row.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group size");
+    if constexpr (N >= 2) x += dpp<kDppQuadXor1>(x);
+    if constexpr (N >= 4) x += dpp<kDppQuadXor2>(x);
+    if constexpr (N >= 8) x += dpp<kDppRowHalfMirror>(x);
+    if constexpr (N >= 16) x += dpp<kDppRowMirror>(x);
+    return x;
+}
+
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group size");
+    if constexpr (N >= 2) x = fmaxf(x, dpp<kDppQuadXor1>(x));
+    if constexpr (N >= 4) x = fmaxf(x, dpp<kDppQuadXor2>(x));
+    if constexpr (N >= 8) x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
+    if constexpr (N >= 16) x = fmaxf(x, dpp<kDppRowMirror>(x));
+    return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+    return x;
+}
+
+// Signed byte b of a dword as float: one v_cvt_f32_i32 with an SDWA
+// sign-extended byte select on gfx950.
+__device__ __forceinline__ float sbyte(int w, int b) {
+    return static_cast<float>(static_cast<int8_t>(w >> (8 * b)));
+}
+
+// 16 int8 values (one int4 load) -> 16 floats.
+__device__ __forceinline__ void unpack16(const int4& x, float (&f)[16]) {
+    const int w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int b = 0; b < 4; b++) f[4 * j + b] = sbyte(w[j], b);
+    }
+}
+
+// v_exp_f32: 2^x, exp2(-inf) == 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------
+// Per-token symmetric int8 quantiser.  scale = amax / 127.0f with IEEE division
+// (HIP's default correctly rounded fp32 divide), q = clamp(rintf(x / scale),
+// -127, 127) with rintf = round half to even (v_rndne_f32); a zero scale (amax
+// == 0, or amax so small that the quotient underflows) stores q = 0.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float quant_scale(float amax) { return amax / 127.0f; }
+
+__device__ __forceinline__ int quant_one(float x, float scale) {
+    if (scale == 0.0f) return 0;
+    float y = __builtin_rintf(x / scale);
+    y = fminf(fmaxf(y, -127.0f), 127.0f);
+    return static_cast<int>(y);
+}
+
+__device__ __forceinline__ int pack4(int a, int b, int c, int d) {
+    return (a & 0xff) | ((b & 0xff) << 8) | ((c & 0xff) << 16) | (static_cast<int>(static_cast<unsigned>(d & 0xff) << 24));
+}
+
+}  // namespace kvq

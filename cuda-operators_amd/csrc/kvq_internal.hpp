@@ -1,0 +1,62 @@
+// kvq_internal.hpp -- host/device shared definitions of libkvq.so (not installed).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace kvq {
+
+// Everything one decode launch needs; passed to the kernels by value.
+struct DecodeArgs {
+    const float* q;          // [B, Hq, d]
+    int8_t* k;               // [B, Hkv, cap, d]
+    int8_t* v;
+    float* ks;               // [B, Hkv, cap]
+    float* vs;
+    float* out;              // [B, Hq, d]
+    const int32_t* lengths;  // [B] or null
+    const float* k_new;      // fused append source [B, Hkv, d] or null
+    const float* v_new;
+    float* part_ml;          // [B, Hq, splits, 2]  (max in log2 units, sum)
+    float* part_acc;         // [B, Hq, splits, d]  unnormalised accumulators
+    int* counters;           // [B * Hkv * nsg] arrival counters, or null (merge kernel)
+    int B, Hq, Hkv, G, cap, d;
+    int uniform_len;         // used when lengths == null
+    int max_len;             // every length is clamped to [0, max_len], max_len <= cap
+    int splits;              // grid splits per sequence
+    int chunk;               // tokens per split
+    int nsg;                 // head groups per kv head (G / heads per workgroup)
+    float scale_log2;        // softmax_scale * log2(e)
+};
+
+// Launch plan chosen on the host.
+struct DecodePlan {
+    bool fast;       // tuned kernel (d in {32,64,128,256}, 16-byte aligned rows)
+    int sg;          // query heads per workgroup (fast path)
+    int nsg;         // G / sg
+    int splits;      // splits per sequence (grid dimension)
+    int chunk;       // tokens per split
+    size_t counter_bytes, ml_bytes, acc_bytes;  // workspace regions (0 when splits == 1)
+};
+
+// Kernel launchers (kvq_decode.hip / kvq_append.hip).  They do no argument
+// validation; the C ABI layer (kvq_capi.cpp) validates before calling them.
+hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& plan, hipStream_t stream);
+hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream);
+// Append one token per (b, kv head).  Position: positions[b] (or uniform_pos
+// when positions is null); with from_lengths, positions holds sequence lengths
+// and the token goes to clamp(lengths[b], 0, max_len) - 1.
+hipError_t launch_append(const float* k_new, const float* v_new, int8_t* k, int8_t* v, float* ks,
+                         float* vs, const int32_t* positions, int uniform_pos, bool from_lengths,
+                         int B, int Hkv, int max_len, int cap, int d, hipStream_t stream);
+hipError_t launch_quantize_rows(const float* x, int64_t rows, int d, int8_t* q, float* scale,
+                                hipStream_t stream);
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
+
+// Tile geometry of the fast kernel for a head dim (tokens one workgroup
+// iteration covers); 0 when the fast kernel does not support d.
+int fast_tile_tokens(int d);
+int fast_heads_per_group(int G);
+
+}  // namespace kvq

@@ -1,0 +1,261 @@
+"""ctypes binding of libkvq.so (include/kvq.h) for torch device tensors.
+
+The operator itself is the C ABI; this module only marshals torch tensors
+(device memory) and torch streams into it.  There is no fallback: if
+libkvq.so is missing or a call fails, an exception is raised.
+
+Entry points mirror the reference's kv_cache/ interface:
+  solve(...)                  -> kv_cache/KV_int8.cu:306 (legacy void ABI, null stream)
+  kv_int8_split_launch(...)   -> kv_cache/KV_int8_split_optimized.cu:268
+  kv_int8_simple_launch(...)  -> kv_cache/new_kvint8.cu:85
+plus the batched / GQA / ragged / append extension (decode, append,
+quantize_rows, workspace helpers).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkvq.so")
+
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+MAX_HEAD_DIM = 4096
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+_vp = ctypes.c_void_p
+_int = ctypes.c_int
+
+
+class DecodeParams(ctypes.Structure):
+    """struct kvq_decode_params (include/kvq.h)."""
+    _fields_ = [
+        ("batch", _int), ("num_q_heads", _int), ("num_kv_heads", _int), ("head_dim", _int),
+        ("capacity", _int), ("max_seq_len", _int),
+        ("lengths", _vp), ("q", _vp), ("k_cache", _vp), ("v_cache", _vp),
+        ("k_scale", _vp), ("v_scale", _vp), ("out", _vp),
+        ("softmax_scale", ctypes.c_float), ("num_splits", _int),
+        ("k_new", _vp), ("v_new", _vp),
+    ]
+
+
+class AppendParams(ctypes.Structure):
+    """struct kvq_append_params (include/kvq.h)."""
+    _fields_ = [
+        ("batch", _int), ("num_kv_heads", _int), ("head_dim", _int), ("capacity", _int),
+        ("positions", _vp), ("uniform_position", _int),
+        ("k_new", _vp), ("v_new", _vp), ("k_cache", _vp), ("v_cache", _vp),
+        ("k_scale", _vp), ("v_scale", _vp),
+    ]
+
+
+EXPORTS = ("solve", "kv_int8_split_launch", "kv_int8_simple_launch", "kvq_decode_workspace_size",
+           "kvq_workspace_init", "kvq_decode_launch", "kvq_append_launch", "kvq_quantize_rows_launch",
+           "kvq_version")
+
+
+class KvqError(RuntimeError):
+    def __init__(self, fn: str, code: int):
+        super().__init__(f"{fn} returned hipError {code}")
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """Load libkvq.so (built in-tree by __graft_entry__.build() / make)."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libkvq.so is not built ({LIB_PATH}); run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        ref = [_vp] * 6 + [_int] * 3
+        L.solve.argtypes = ref
+        L.solve.restype = None
+        for fn in ("kv_int8_split_launch", "kv_int8_simple_launch"):
+            getattr(L, fn).argtypes = ref + [_vp, _vp]
+            getattr(L, fn).restype = _int
+        L.kvq_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeParams)]
+        L.kvq_decode_workspace_size.restype = ctypes.c_size_t
+        L.kvq_workspace_init.argtypes = [_vp, ctypes.c_size_t, _vp]
+        L.kvq_workspace_init.restype = _int
+        L.kvq_decode_launch.argtypes = [ctypes.POINTER(DecodeParams), _vp, ctypes.c_size_t, _vp]
+        L.kvq_decode_launch.restype = _int
+        L.kvq_append_launch.argtypes = [ctypes.POINTER(AppendParams), _vp]
+        L.kvq_append_launch.restype = _int
+        L.kvq_quantize_rows_launch.argtypes = [_vp, ctypes.c_int64, _int, _vp, _vp, _vp]
+        L.kvq_quantize_rows_launch.restype = _int
+        L.kvq_version.restype = ctypes.c_char_p
+        _lib = L
+        return L
+
+
+def version() -> str:
+    return lib().kvq_version().decode()
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _check(fn: str, code: int) -> None:
+    if code != HIP_SUCCESS:
+        raise KvqError(fn, code)
+
+
+def _need(t, dtype, shape, name):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch tensor")
+    if t.dtype != dtype or tuple(t.shape) != tuple(shape) or not t.is_contiguous() or t.device.type != "cuda":
+        raise ValueError(f"{name}: want contiguous cuda {dtype} {tuple(shape)}, got {t.dtype} "
+                         f"{tuple(t.shape)} on {t.device}")
+
+
+# ---------------------------------------------------------------------------
+# reference ABI
+# ---------------------------------------------------------------------------
+def solve(Q, K, V, k_scale, v_scale, out) -> None:
+    """Legacy `solve` on the null stream: Q[H,d], K/V[H,N,d] int8, scales[H,N], out[H,d]."""
+    H, N, d = K.shape
+    lib().solve(_ptr(Q), _ptr(K), _ptr(V), _ptr(k_scale), _ptr(v_scale), _ptr(out), H, N, d)
+
+
+def kv_int8_split_launch(Q, K, V, k_scale, v_scale, out, S, stream=None, simple=False) -> int:
+    """Stream-aware reference launch; S is H*N floats of caller scratch. Returns the hipError code."""
+    H, N, d = K.shape
+    fn = lib().kv_int8_simple_launch if simple else lib().kv_int8_split_launch
+    return int(fn(_ptr(Q), _ptr(K), _ptr(V), _ptr(k_scale), _ptr(v_scale), _ptr(out), H, N, d, _ptr(S),
+                  _stream(stream)))
+
+
+# ---------------------------------------------------------------------------
+# extension
+# ---------------------------------------------------------------------------
+def decode_params(q, k_cache, v_cache, k_scale, v_scale, out, lengths=None, max_seq_len=0,
+                  softmax_scale=0.0, num_splits=0, k_new=None, v_new=None) -> DecodeParams:
+    B, Hq, d = q.shape
+    _, Hkv, cap, _ = k_cache.shape
+    return DecodeParams(B, Hq, Hkv, d, cap, int(max_seq_len), _ptr(lengths), _ptr(q), _ptr(k_cache),
+                        _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(out), float(softmax_scale),
+                        int(num_splits), _ptr(k_new), _ptr(v_new))
+
+
+def workspace_size(p: DecodeParams) -> int:
+    return int(lib().kvq_decode_workspace_size(ctypes.byref(p)))
+
+
+def workspace_init(ws, nbytes=None, stream=None) -> None:
+    nbytes = ws.numel() * ws.element_size() if nbytes is None else nbytes
+    _check("kvq_workspace_init", lib().kvq_workspace_init(_ptr(ws), nbytes, _stream(stream)))
+
+
+def new_workspace(p: DecodeParams, device=None, stream=None) -> torch.Tensor:
+    """Allocate and zero-fill a workspace for params p (an empty tensor when none is needed)."""
+    n = workspace_size(p)
+    ws = torch.empty(max(n, 1), dtype=torch.uint8, device=device or "cuda")
+    if n:
+        workspace_init(ws, n, stream)
+    return ws
+
+
+def decode_launch(p: DecodeParams, ws, stream=None) -> None:
+    nbytes = 0 if ws is None else ws.numel() * ws.element_size()
+    _check("kvq_decode_launch", lib().kvq_decode_launch(ctypes.byref(p), _ptr(ws), nbytes, _stream(stream)))
+
+
+class Decoder:
+    """A decode problem with its own workspace: build once, launch many times."""
+
+    def __init__(self, q, k_cache, v_cache, k_scale, v_scale, out, lengths=None, max_seq_len=0,
+                 softmax_scale=0.0, num_splits=0, k_new=None, v_new=None, stream=None):
+        B, Hq, d = q.shape
+        _, Hkv, cap, d2 = k_cache.shape
+        if d2 != d or Hq % Hkv:
+            raise ValueError("shape mismatch")
+        _need(q, torch.float32, (B, Hq, d), "q")
+        for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+            _need(t, torch.int8, (B, Hkv, cap, d), n)
+        for t, n in ((k_scale, "k_scale"), (v_scale, "v_scale")):
+            _need(t, torch.float32, (B, Hkv, cap), n)
+        _need(out, torch.float32, (B, Hq, d), "out")
+        if lengths is not None:
+            _need(lengths, torch.int32, (B,), "lengths")
+        if k_new is not None:
+            _need(k_new, torch.float32, (B, Hkv, d), "k_new")
+            _need(v_new, torch.float32, (B, Hkv, d), "v_new")
+        self.keep = (q, k_cache, v_cache, k_scale, v_scale, out, lengths, k_new, v_new)
+        self.params = decode_params(q, k_cache, v_cache, k_scale, v_scale, out, lengths, max_seq_len,
+                                    softmax_scale, num_splits, k_new, v_new)
+        self.ws = new_workspace(self.params, q.device, stream)
+        self.ws_bytes = workspace_size(self.params)
+
+    def __call__(self, stream=None) -> None:
+        _check("kvq_decode_launch",
+               lib().kvq_decode_launch(ctypes.byref(self.params), _ptr(self.ws), self.ws_bytes,
+                                       _stream(stream)))
+
+
+def decode(q, k_cache, v_cache, k_scale, v_scale, lengths=None, max_seq_len=0, softmax_scale=0.0,
+           num_splits=0, k_new=None, v_new=None, out=None, stream=None) -> torch.Tensor:
+    """One-shot batched decode attention; returns out[B, Hq, d]."""
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    Decoder(q, k_cache, v_cache, k_scale, v_scale, out, lengths, max_seq_len, softmax_scale, num_splits,
+            k_new, v_new, stream)(stream)
+    return out
+
+
+def append(k_new, v_new, k_cache, v_cache, k_scale, v_scale, positions=None, uniform_position=0,
+           stream=None) -> None:
+    B, Hkv, cap, d = k_cache.shape
+    p = AppendParams(B, Hkv, d, cap, _ptr(positions), int(uniform_position), _ptr(k_new), _ptr(v_new),
+                     _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale))
+    _check("kvq_append_launch", lib().kvq_append_launch(ctypes.byref(p), _stream(stream)))
+
+
+def quantize_rows(x, q=None, scale=None, stream=None):
+    """x[..., d] fp32 cuda -> (q int8 [..., d], scale fp32 [...])."""
+    d = x.shape[-1]
+    rows = x.numel() // d if d else 0
+    if q is None:
+        q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    if scale is None:
+        scale = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    _check("kvq_quantize_rows_launch",
+           lib().kvq_quantize_rows_launch(_ptr(x), rows, d, _ptr(q), _ptr(scale), _stream(stream)))
+    return q, scale
+
+
+def default_softmax_scale(d: int) -> float:
+    """1/sqrtf(d) in fp32, as kv_cache/KV_int8_split_optimized.cu:335."""
+    import numpy as np
+    return float(np.float32(1.0) / np.sqrt(np.float32(d)))
+
+
+def kv_bytes(lengths, num_kv_heads: int, head_dim: int) -> int:
+    """Algorithmic KV-cache bytes one decode step reads: sum_b len_b * Hkv * (2*d + 8)."""
+    total = int(sum(int(x) for x in lengths))
+    return total * num_kv_heads * (2 * head_dim + 8)
+
+
+__all__ = ["lib", "version", "solve", "kv_int8_split_launch", "DecodeParams", "AppendParams", "Decoder",
+           "decode", "decode_params", "decode_launch", "workspace_size", "workspace_init", "new_workspace",
+           "append", "quantize_rows", "kv_bytes", "KvqError", "EXPORTS"]

@@ -1,0 +1,151 @@
+/*
+ * kvq.h -- C ABI of libkvq.so, the MI355X (gfx950) INT8 KV-cache
+ * decode-attention operator.
+ *
+ * Part 1 is the drop-in boundary: the exact extern "C" symbols of the
+ * reference's kv_cache/ path (Murmurwkk/cuda-operators), with HIP types in
+ * place of CUDA ones (hipSuccess == cudaSuccess == 0,
+ * hipErrorInvalidValue == cudaErrorInvalidValue == 1).  One library exports
+ * one `solve`; the reference's four kv_cache .cu files each export their own
+ * and cannot be linked together.
+ *
+ * Part 2 is the extension the reference lacks (batch, grouped-query heads,
+ * ragged lengths, sequence splits with a log-sum-exp merge, appending a
+ * quantised token).  Each query head hq of batch b computes exactly the
+ * reference's single-head math over kv head hq / (Hq/Hkv) and the first
+ * lengths[b] tokens.
+ *
+ * Layouts (row-major, contiguous; all pointers are device pointers):
+ *   reference ABI:  Q[H,d] fp32, K/V[H,N,d] int8, k/v_scale[H,N] fp32, out[H,d]
+ *   extension:      q[B,Hq,d], k/v cache[B,Hkv,cap,d] int8,
+ *                   k/v scale[B,Hkv,cap] fp32, out[B,Hq,d], lengths[B] int32
+ *
+ * Math (both parts): s_t = (sum_i q_i * K[t,i]) * k_scale[t] * softmax_scale,
+ * p = softmax(s), out_i = sum_t p_t * (V[t,i] * v_scale[t]); softmax_scale
+ * defaults to 1/sqrtf(d) as in the reference.
+ */
+#ifndef KVQ_H
+#define KVQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Largest head_dim any entry point accepts (head_dim in {32,64,128,256} runs
+ * the tuned kernels; any other value up to this bound runs a generic kernel). */
+#define KVQ_MAX_HEAD_DIM 4096
+
+/* ===================== Part 1: reference entry points ===================== */
+
+/* Replaces `solve`, kv_cache/KV_int8.cu:306-316 (also KV_int8_single_buffer.cu:260-270,
+ * KV_int8_split_optimized.cu:294-304, new_kvint8.cu:102-104).
+ * Legacy void ABI: invalid arguments print one line to stderr and return
+ * without device work (as KV_int8_split_optimized.cu:306-324).  Runs
+ * asynchronously on the null stream.  Split workspace comes from a per-device
+ * cache owned by the library (allocated on first use, grown when needed). */
+void solve(const float* Q, const int8_t* K_int8, const int8_t* V_int8,
+           const float* k_scale, const float* v_scale, float* output,
+           int num_heads, int seq_len, int head_dim);
+
+/* Replaces `kv_int8_split_launch`, kv_cache/KV_int8_split_optimized.cu:266-292.
+ * S is caller-owned scratch of at least num_heads*seq_len floats; it holds the
+ * per-split partial (max, sum, acc[d]) records, so at most seq_len/(head_dim+2)
+ * splits per head are used (1 split needs no scratch at all).
+ * Returns hipErrorInvalidValue, before any HIP call, for a null pointer,
+ * num_heads/seq_len/head_dim <= 0 or head_dim > KVQ_MAX_HEAD_DIM; otherwise the
+ * launch status.  Asynchronous on `stream`; the caller checks completion. */
+hipError_t kv_int8_split_launch(const float* Q, const int8_t* K_int8, const int8_t* V_int8,
+                                const float* k_scale, const float* v_scale, float* output,
+                                int num_heads, int seq_len, int head_dim, float* S,
+                                hipStream_t stream);
+
+/* Replaces `kv_int8_simple_launch`, kv_cache/new_kvint8.cu:83-100 (identical
+ * signature and contract to kv_int8_split_launch; same kernels here). */
+hipError_t kv_int8_simple_launch(const float* Q, const int8_t* K_int8, const int8_t* V_int8,
+                                 const float* k_scale, const float* v_scale, float* output,
+                                 int num_heads, int seq_len, int head_dim, float* S,
+                                 hipStream_t stream);
+
+/* ============== Part 2: extension (no counterpart in the reference) ============== */
+
+typedef struct kvq_decode_params {
+    int batch;             /* B  >= 1 */
+    int num_q_heads;       /* Hq >= 1, a multiple of num_kv_heads */
+    int num_kv_heads;      /* Hkv >= 1 */
+    int head_dim;          /* d in [1, KVQ_MAX_HEAD_DIM] */
+    int capacity;          /* token stride of one (b, kv_head) cache row block, >= 1 */
+    int max_seq_len;       /* uniform length when lengths == NULL; otherwise an upper
+                              bound on every lengths[b] (0 means capacity) */
+    const int32_t* lengths;/* device [B] or NULL; each clamped on device to
+                              [0, max_seq_len] (max_seq_len 0: capacity);
+                              a sequence of length 0 yields a zero output row */
+    const float* q;        /* [B, Hq, d] */
+    int8_t* k_cache;       /* [B, Hkv, capacity, d]; written only by a fused append */
+    int8_t* v_cache;
+    float* k_scale;        /* [B, Hkv, capacity] */
+    float* v_scale;
+    float* out;            /* [B, Hq, d], fully overwritten */
+    float softmax_scale;   /* <= 0 selects 1/sqrtf(d) */
+    int num_splits;        /* 0 = choose; otherwise the split count per sequence */
+    /* Fused append (both NULL = off).  When set, token length_b - 1 of every
+     * (b, kv_head) is first quantised from k_new/v_new [B, Hkv, d] fp32 into the
+     * cache (int8 values + scale, the same bits as kvq_append_launch), then
+     * attended over; the caller's lengths already count the new token. */
+    const float* k_new;
+    const float* v_new;
+} kvq_decode_params;
+
+/* Bytes of workspace kvq_decode_launch needs for `p` (0 when one split
+ * suffices).  The workspace holds per-split partials and one arrival counter
+ * per (b, kv_head, head group); it must be zero-filled once after allocation
+ * (kvq_workspace_init) and is left zeroed by every completed launch.  Calls
+ * that overlap in time must not share a workspace. */
+size_t kvq_decode_workspace_size(const kvq_decode_params* p);
+
+/* Zero-fills a workspace on `stream` with a fill kernel (no hipMemset). */
+hipError_t kvq_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Decode attention (plus the optional fused append) in one kernel launch:
+ * splits write partial (max, sum, acc) records and the last split of each
+ * sequence to finish merges them with a log-sum-exp reduction.
+ * Returns hipErrorInvalidValue before any HIP call on a bad argument or a
+ * workspace smaller than kvq_decode_workspace_size(p). */
+hipError_t kvq_decode_launch(const kvq_decode_params* p, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+
+typedef struct kvq_append_params {
+    int batch, num_kv_heads, head_dim, capacity;
+    const int32_t* positions; /* device [B] write position per sequence, or NULL */
+    int uniform_position;     /* used when positions == NULL */
+    const float* k_new;       /* [B, Hkv, d] fp32 */
+    const float* v_new;
+    int8_t* k_cache;          /* [B, Hkv, capacity, d] */
+    int8_t* v_cache;
+    float* k_scale;           /* [B, Hkv, capacity] */
+    float* v_scale;
+} kvq_append_params;
+
+/* Quantises one new K and V token per (b, kv_head): scale = max|x|/127.0f
+ * (IEEE division), q = clamp(rintf(x/scale), -127, 127); a zero (or
+ * underflowing) scale stores 0 and all-zero int8.  Positions outside
+ * [0, capacity) are skipped.  lengths are not modified. */
+hipError_t kvq_append_launch(const kvq_append_params* p, hipStream_t stream);
+
+/* Bulk (prefill) quantiser: x[rows, d] fp32 -> q[rows, d] int8 + scale[rows],
+ * the same per-row rule as kvq_append_launch. */
+hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, int8_t* q,
+                                    float* scale, hipStream_t stream);
+
+/* Library version string, e.g. "kvq 0.1.0 gfx950". */
+const char* kvq_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVQ_H */

@@ -1,0 +1,124 @@
+"""The quantisers on the GPU, bit-exact against the CPU oracle.
+
+The reference has no quantiser (kv_cache/new_kvint8.cu:83-84); the rule is
+the task spec (scale = max|x|/127, int8 = round(x/scale) clamped to +-127) with
+the decisions fixed in the oracle: IEEE division, round half to even, zero or
+underflowing scale -> zero row.  Int8 values and scale bits must match exactly.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import _gpu
+from _gpu import down, kvq, up
+from _util import student_t4
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def crafted_rows(d):
+    rng = np.random.default_rng(d)
+    rows = []
+    r = np.zeros(d, np.float32)
+    r[:8] = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5]  # exact ties (scale 1.0)
+    rows.append(r)
+    r = np.full(d, 0.25, np.float32)
+    r[-1] = -254.0                                           # amax negative, last index
+    rows.append(r)
+    rows.append(np.zeros(d, np.float32))                     # zero row
+    r = np.zeros(d, np.float32)
+    r[:3] = [1e-44, -2e-44, 5e-45]                           # scale underflows to 0
+    rows.append(r)
+    rows.append(rng.standard_normal(d, dtype=np.float32) * np.float32(1e-38))  # subnormal scale
+    r = rng.standard_normal(d, dtype=np.float32)
+    r[0] = 1e30                                              # huge outlier at index 0
+    rows.append(r)
+    # ties at a non-unit scale: amax = 254 -> scale = 2.0, x = 2*(k + 0.5)
+    r = np.zeros(d, np.float32)
+    r[0] = 254.0
+    r[1:6] = [1.0, 3.0, 5.0, -7.0, 9.0]
+    rows.append(r)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("d", [16, 64, 100, 128, 256])
+def test_quantize_rows_bit_exact(d):
+    o = orc.get()
+    rng = np.random.default_rng(d + 1)
+    x = np.concatenate([crafted_rows(d), rng.standard_normal((500, d), dtype=np.float32),
+                        student_t4(rng, (300, d)), rng.standard_normal((50, d), dtype=np.float32) * np.float32(1e4)])
+    gq, gs = kvq.quantize_rows(up(x))
+    torch.cuda.synchronize()
+    wq, ws = o.quantize_rows(x)
+    assert np.array_equal(down(gq), wq)
+    assert np.array_equal(_bits(down(gs)), _bits(ws))
+
+
+def test_quantize_golden_fixture():
+    g = np.load(os.path.join(GOLD, "quant.npz"), allow_pickle=False)
+    gq, gs = kvq.quantize_rows(up(g["x"]))
+    torch.cuda.synchronize()
+    assert np.array_equal(down(gq), g["q"]) and np.array_equal(_bits(down(gs)), _bits(g["scale"]))
+
+
+def test_quantize_many_rows():
+    """A bulk prefill-sized tensor (grid-stride path) stays bit-exact."""
+    o = orc.get()
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4, 8, 4096, 128), dtype=np.float32)
+    gq, gs = kvq.quantize_rows(up(x))
+    torch.cuda.synchronize()
+    wq, ws = o.quantize_rows(x)
+    assert np.array_equal(down(gq), wq) and np.array_equal(_bits(down(gs)), _bits(ws))
+
+
+@pytest.mark.parametrize("d", [64, 128, 100])
+def test_append_bit_exact_and_positions(d):
+    o = orc.get()
+    rng = np.random.default_rng(d)
+    B, Hkv, cap = 4, 3, 50
+    k = rng.integers(-127, 128, (B, Hkv, cap, d), dtype=np.int8)
+    v = rng.integers(-127, 128, (B, Hkv, cap, d), dtype=np.int8)
+    ks = rng.uniform(0.01, 0.1, (B, Hkv, cap)).astype(np.float32)
+    vs = rng.uniform(0.01, 0.1, (B, Hkv, cap)).astype(np.float32)
+    kn = np.concatenate([crafted_rows(d)[:Hkv][None], rng.standard_normal((B - 1, Hkv, d), dtype=np.float32)])
+    vn = student_t4(rng, (B, Hkv, d))
+    pos = np.array([0, cap - 1, cap, 17], np.int32)  # cap is out of range: skipped
+    gk, gv, gks, gvs = up(k), up(v), up(ks), up(vs)
+    kvq.append(up(kn), up(vn), gk, gv, gks, gvs, positions=up(pos))
+    torch.cuda.synchronize()
+    o.append(kn, vn, k, v, ks, vs, positions=pos)
+    assert np.array_equal(down(gk), k) and np.array_equal(down(gv), v)
+    assert np.array_equal(_bits(down(gks)), _bits(ks)) and np.array_equal(_bits(down(gvs)), _bits(vs))
+    # uniform position
+    kvq.append(up(kn), up(vn), gk, gv, gks, gvs, positions=None, uniform_position=5)
+    torch.cuda.synchronize()
+    o.append(kn, vn, k, v, ks, vs, positions=None, uniform_pos=5)
+    assert np.array_equal(down(gk), k) and np.array_equal(_bits(down(gvs)), _bits(vs))
+
+
+def test_append_cfg4_shape():
+    """One appended token per (b, kv head) at config 4's shape (B256, Hkv8, d128)."""
+    o = orc.get()
+    rng = np.random.default_rng(44)
+    B, Hkv, cap, d = 256, 8, 8, 128
+    k = np.zeros((B, Hkv, cap, d), np.int8)
+    v = np.zeros_like(k)
+    ks = np.zeros((B, Hkv, cap), np.float32)
+    vs = np.zeros_like(ks)
+    kn, vn = student_t4(rng, (B, Hkv, d)), student_t4(rng, (B, Hkv, d))
+    pos = rng.integers(0, cap, B).astype(np.int32)
+    gk, gv, gks, gvs = up(k), up(v), up(ks), up(vs)
+    kvq.append(up(kn), up(vn), gk, gv, gks, gvs, positions=up(pos))
+    torch.cuda.synchronize()
+    o.append(kn, vn, k, v, ks, vs, positions=pos)
+    assert np.array_equal(down(gk), k) and np.array_equal(down(gv), v)
+    assert np.array_equal(_bits(down(gks)), _bits(ks)) and np.array_equal(_bits(down(gvs)), _bits(vs))
