@@ -21,9 +21,19 @@ using kvq::DecodePlan;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr size_t kAlign = 256;
+// Arrival counters live in a fixed-size prefix of every workspace, so a
+// workspace zero-filled once stays valid for any later problem shape: the
+// counters are only ever written as counters (and left at zero), partial
+// records always start after the prefix.  Problems with more sequence groups
+// than counters use the separate merge kernel instead.
+constexpr size_t kCounterBytes = 256 * 1024;
+constexpr long kMaxCounters = static_cast<long>(kCounterBytes / sizeof(int));
 // Workgroups a decode launch aims for when it picks the split count itself:
 // 8 per CU on MI355X's 256 CUs.
-constexpr int kTargetWorkgroups = 2048;
+#ifndef KVQ_TARGET_WG
+#define KVQ_TARGET_WG 256
+#endif
+constexpr int kTargetWorkgroups = KVQ_TARGET_WG;
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -36,9 +46,10 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, i
                      int max_splits, bool fused) {
     DecodePlan p{};
     const int G = Hq / Hkv;
-    const int tile = kvq::fast_tile_tokens(d);
+    const int sg = kvq::fast_heads_per_group(G);
+    const int tile = kvq::fast_tile_tokens(d, sg);
     p.fast = tile > 0 && aligned;
-    p.sg = p.fast ? kvq::fast_heads_per_group(G) : 1;
+    p.sg = p.fast ? sg : 1;
     p.nsg = p.fast ? G / p.sg : G;
     const long units = p.fast ? static_cast<long>(B) * Hkv * p.nsg : static_cast<long>(B) * Hq;
     const int gran = p.fast ? tile : 64;
@@ -60,7 +71,11 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, i
     p.splits = (max_len + chunk - 1) / chunk;
     if (p.splits > 1) {
         const size_t recs = static_cast<size_t>(B) * Hq * p.splits;
-        p.counter_bytes = (fused && p.fast) ? round_up(sizeof(int) * static_cast<size_t>(units), kAlign) : 0;
+        // A workspace in fused layout always reserves the counter prefix, even
+        // for a plan that merges with the separate kernel, so partial records
+        // can never land on another plan's counters.
+        p.counter_bytes = fused ? kCounterBytes : 0;
+        p.counters = fused && p.fast && units <= kMaxCounters;
         p.ml_bytes = round_up(recs * 2 * sizeof(float), kAlign);
         p.acc_bytes = round_up(recs * static_cast<size_t>(d) * sizeof(float), kAlign);
     }
@@ -71,7 +86,7 @@ size_t plan_bytes(const DecodePlan& p) { return p.counter_bytes + p.ml_bytes + p
 
 void bind_workspace(DecodeArgs& a, const DecodePlan& p, void* ws) {
     char* base = static_cast<char*>(ws);
-    a.counters = p.counter_bytes ? reinterpret_cast<int*>(base) : nullptr;
+    a.counters = p.counters ? reinterpret_cast<int*>(base) : nullptr;
     a.part_ml = p.splits > 1 ? reinterpret_cast<float*>(base + p.counter_bytes) : nullptr;
     a.part_acc = p.splits > 1 ? reinterpret_cast<float*>(base + p.counter_bytes + p.ml_bytes) : nullptr;
 }

@@ -36,15 +36,24 @@
 namespace kvq {
 namespace {
 
-constexpr int kFastWaves = 4;  // waves per workgroup
-constexpr int kFastU = 4;      // tokens per lane group per loop iteration
+#ifndef KVQ_FAST_WAVES
+#define KVQ_FAST_WAVES 8
+#endif
+constexpr int kFastWaves = KVQ_FAST_WAVES;  // waves per workgroup
 
-template <int D>
+// Tile geometry: D/16 lanes share a token (16 bytes each); U tokens per lane
+// group per loop iteration (fewer when SG query heads already hold 2*16*SG
+// registers of q and accumulators).
+template <int D, int SG>
 struct FastGeom {
-    static constexpr int LPT = D / 16;          // lanes per token
-    static constexpr int TPL = kWave / LPT;     // tokens per wave load
-    static constexpr int WSTEP = TPL * kFastU;  // tokens per wave iteration
-    static constexpr int BSTEP = WSTEP * kFastWaves;
+    static constexpr int LPT = D / 16;                // lanes per token
+    static constexpr int TPL = kWave / LPT;           // tokens per wave load
+    static constexpr int U = SG >= 4 ? 2 : 4;         // tokens per lane group per iteration
+    // Software pipelining (next tile's loads in flight during compute) pays
+    // for SG = 4; at SG <= 2 the extra registers cost more than it hides.
+    static constexpr bool PIPE = SG >= 4;
+    static constexpr int WSTEP = TPL * U;             // tokens per wave iteration
+    static constexpr int BSTEP = WSTEP * kFastWaves;  // tokens per workgroup iteration
 };
 
 __device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
@@ -52,17 +61,52 @@ __device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
     return min(max(len, 0), a.max_len);
 }
 
+// U consecutive per-token scales (U in {1,2,4,8}); p is U*4-byte aligned when
+// the token index is a multiple of U (tiles start at multiples of U tokens).
+template <int U>
+__device__ __forceinline__ void load_scales(const float* p, float (&out)[U]) {
+    if constexpr (U % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < U; i += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(p + i);
+            out[i] = x.x;
+            out[i + 1] = x.y;
+            out[i + 2] = x.z;
+            out[i + 3] = x.w;
+        }
+    } else if constexpr (U == 2) {
+        const float2 x = *reinterpret_cast<const float2*>(p);
+        out[0] = x.x;
+        out[1] = x.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < U; i++) out[i] = p[i];
+    }
+}
+
+// Partial records cross workgroups (and XCDs, whose L2s are not coherent with
+// each other) inside one launch.  They are written and read with agent-scope
+// relaxed atomics, i.e. device-coherent global_store/global_load sc1, so no
+// L2-wide writeback/invalidate fence is needed; the producer waits for its
+// stores to complete (s_waitcnt 0) before it bumps the arrival counter.
+__device__ __forceinline__ void put_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float get_coherent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Log-sum-exp merge of the nsplit partial records of output row bhq, element dim.
 __device__ float merge_dim(const DecodeArgs& a, size_t bhq, int dim, int nsplit) {
     const float* ml = a.part_ml + bhq * a.splits * 2;
     const float* acc = a.part_acc + bhq * a.splits * a.d;
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, ml[2 * s]);
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, get_coherent(ml + 2 * s));
     float L = 0.0f, A = 0.0f;
     for (int s = 0; s < nsplit; s++) {
-        const float w = fast_exp2(ml[2 * s] - M);
-        L = fmaf(ml[2 * s + 1], w, L);
-        A = fmaf(acc[static_cast<size_t>(s) * a.d + dim], w, A);
+        const float w = fast_exp2(get_coherent(ml + 2 * s) - M);
+        L = fmaf(get_coherent(ml + 2 * s + 1), w, L);
+        A = fmaf(get_coherent(acc + static_cast<size_t>(s) * a.d + dim), w, A);
     }
     return A / L;
 }
@@ -121,12 +165,16 @@ __device__ __forceinline__ void attend(const float (&qr)[SG][16], const int4 (&k
 
 template <int D, int SG>
 __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArgs a) {
-    using Geo = FastGeom<D>;
+    using Geo = FastGeom<D, SG>;
     constexpr int LPT = Geo::LPT;
-    constexpr int TPL = Geo::TPL;
-    constexpr int U = kFastU;
+    constexpr int U = Geo::U;
+    constexpr int NT = kFastWaves * kWave;
+    constexpr int NE = (2 * D + NT - 1) / NT;  // appended K+V elements per thread
     __shared__ float s_ml[kFastWaves][SG][2];
     __shared__ float s_acc[kFastWaves][SG][D];
+    __shared__ float s_amax[2][kFastWaves];
+    __shared__ float s_newscale[2];
+    __shared__ __align__(16) int s_newq[2][D / 4];  // appended K and V rows, packed int8
     __shared__ int s_last;
 
     const int lane = threadIdx.x & (kWave - 1);
@@ -158,6 +206,17 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     const bool app = (a.k_new != nullptr) && (t1 == len);
     const int tend = app ? t1 - 1 : t1;  // tokens read from the cache
 
+    // Fused append, part 1: fetch the new token (element e of the K row then
+    // the V row per thread) now, so the loads overlap the main loop.
+    float xnew[NE];
+#pragma unroll
+    for (int j = 0; j < NE; j++) {
+        const int e = threadIdx.x + j * NT;
+        xnew[j] = 0.0f;
+        if (app && e < 2 * D)
+            xnew[j] = (e < D ? a.k_new : a.v_new)[static_cast<size_t>(bh) * D + (e < D ? e : e - D)];
+    }
+
     float qr[SG][16];
 #pragma unroll
     for (int h = 0; h < SG; h++) {
@@ -186,67 +245,124 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     const float* ksp = a.ks + row0;
     const float* vsp = a.vs + row0;
 
-    for (int base = t0 + wave * Geo::WSTEP; base < tend; base += Geo::BSTEP) {
-        int4 kk[U], vv[U];
-        float kscl[U], vscl[U];
-        bool ok[U];
+    // Main loop.  Lane group tg owns the U consecutive tokens base + tg*U + u,
+    // so each 16-byte K/V load instruction still covers whole 128-byte rows
+    // and the U scales of a lane group come in one 16-byte load per scale
+    // array.  With PIPE the loads of a wave's next tile are in flight while
+    // the current tile is computed.
+    struct Tile {
+        int4 k[U], v[U];
+        float ks[U], vs[U];
+    };
+    auto load_tile = [&](Tile& T, int base) {
+        const int t_first = base + tg * U;
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int t = base + u * TPL + tg;
-            ok[u] = t < tend;
-            const int tc = ok[u] ? t : tend - 1;
-            kk[u] = *reinterpret_cast<const int4*>(kp + static_cast<size_t>(tc) * D);
-            vv[u] = *reinterpret_cast<const int4*>(vp + static_cast<size_t>(tc) * D);
-            kscl[u] = ksp[tc];
-            vscl[u] = vsp[tc];
+            const int tc = min(t_first + u, tend - 1);
+            T.k[u] = load16_stream(kp + static_cast<size_t>(tc) * D);
+            T.v[u] = load16_stream(vp + static_cast<size_t>(tc) * D);
         }
-        attend<SG, U, LPT>(qr, kk, vv, kscl, vscl, ok, a.scale_log2, m, l, acc);
-    }
-
-    if (app && wave == 0) {
-        // Quantise the appended token (same rule and bits as append_kernel),
-        // store it once per kv head, and attend to it from registers.
-        const float4* kn = reinterpret_cast<const float4*>(a.k_new + static_cast<size_t>(bh) * D + ds * 16);
-        const float4* vn = reinterpret_cast<const float4*>(a.v_new + static_cast<size_t>(bh) * D + ds * 16);
-        float xk[16], xv[16];
+        const float* ksu = ksp + t_first;
+        const float* vsu = vsp + t_first;
+        const bool vec_ok = ((reinterpret_cast<uintptr_t>(ksu) | reinterpret_cast<uintptr_t>(vsu)) &
+                             (sizeof(float) * U - 1)) == 0;
+        if (t_first + U <= tend && vec_ok) {
+            load_scales<U>(ksu, T.ks);
+            load_scales<U>(vsu, T.vs);
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float4 x = kn[j], y = vn[j];
-            xk[4 * j] = x.x; xk[4 * j + 1] = x.y; xk[4 * j + 2] = x.z; xk[4 * j + 3] = x.w;
-            xv[4 * j] = y.x; xv[4 * j + 1] = y.y; xv[4 * j + 2] = y.z; xv[4 * j + 3] = y.w;
-        }
-        float ak = 0.0f, av = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            ak = fmaxf(ak, fabsf(xk[j]));
-            av = fmaxf(av, fabsf(xv[j]));
-        }
-        ak = group_max<LPT>(ak);
-        av = group_max<LPT>(av);
-        const float sk = quant_scale(ak), sv = quant_scale(av);
-        int qk[16], qv[16];
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            qk[j] = quant_one(xk[j], sk);
-            qv[j] = quant_one(xv[j], sv);
-        }
-        int4 kk1[1], vv1[1];
-        kk1[0] = make_int4(pack4(qk[0], qk[1], qk[2], qk[3]), pack4(qk[4], qk[5], qk[6], qk[7]),
-                           pack4(qk[8], qk[9], qk[10], qk[11]), pack4(qk[12], qk[13], qk[14], qk[15]));
-        vv1[0] = make_int4(pack4(qv[0], qv[1], qv[2], qv[3]), pack4(qv[4], qv[5], qv[6], qv[7]),
-                           pack4(qv[8], qv[9], qv[10], qv[11]), pack4(qv[12], qv[13], qv[14], qv[15]));
-        const int tnew = len - 1;
-        if (sgi == 0 && tg == 0) {
-            *reinterpret_cast<int4*>(a.k + (row0 + tnew) * D + ds * 16) = kk1[0];
-            *reinterpret_cast<int4*>(a.v + (row0 + tnew) * D + ds * 16) = vv1[0];
-            if (ds == 0) {
-                a.ks[row0 + tnew] = sk;
-                a.vs[row0 + tnew] = sv;
+            for (int u = 0; u < U; u++) {
+                const int tc = min(t_first + u, tend - 1);
+                T.ks[u] = ksp[tc];
+                T.vs[u] = vsp[tc];
             }
         }
-        const float sk1[1] = {sk}, sv1[1] = {sv};
-        const bool ok1[1] = {tg == 0};
-        attend<SG, 1, LPT>(qr, kk1, vv1, sk1, sv1, ok1, a.scale_log2, m, l, acc);
+    };
+    auto run_tile = [&](const Tile& T, int base) {
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) ok[u] = base + tg * U + u < tend;
+        attend<SG, U, LPT>(qr, T.k, T.v, T.ks, T.vs, ok, a.scale_log2, m, l, acc);
+    };
+    int base = t0 + wave * Geo::WSTEP;
+    if constexpr (!Geo::PIPE) {
+        for (; base < tend; base += Geo::BSTEP) {
+            Tile tt;
+            load_tile(tt, base);
+            run_tile(tt, base);
+        }
+    } else {
+        Tile ta, tb;
+        if (base < tend) load_tile(ta, base);
+        while (base < tend) {
+            int nb = base + Geo::BSTEP;
+            if (nb < tend) load_tile(tb, nb);
+            run_tile(ta, base);
+            base = nb;
+            if (base >= tend) break;
+            nb = base + Geo::BSTEP;
+            if (nb < tend) load_tile(ta, nb);
+            run_tile(tb, base);
+            base = nb;
+        }
+    }
+
+    if (app) {
+        // Fused append, part 2: per-row max|x| over the workgroup, the scale,
+        // one quantised element per thread (same rule and bits as
+        // append_kernel), rows handed over through LDS.
+        float mk = 0.0f, mv = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NE; j++) {
+            const int e = threadIdx.x + j * NT;
+            if (e < D) mk = fmaxf(mk, fabsf(xnew[j]));
+            else if (e < 2 * D) mv = fmaxf(mv, fabsf(xnew[j]));
+        }
+        mk = wave_max(mk);
+        mv = wave_max(mv);
+        if (lane == 0) {
+            s_amax[0][wave] = mk;
+            s_amax[1][wave] = mv;
+        }
+        __syncthreads();
+        float ak = 0.0f, av = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kFastWaves; w++) {
+            ak = fmaxf(ak, s_amax[0][w]);
+            av = fmaxf(av, s_amax[1][w]);
+        }
+        const float sk = quant_scale(ak), sv = quant_scale(av);
+#pragma unroll
+        for (int j = 0; j < NE; j++) {
+            const int e = threadIdx.x + j * NT;
+            if (e < 2 * D) {
+                const int row = e < D ? 0 : 1;
+                reinterpret_cast<int8_t*>(s_newq[row])[e - row * D] =
+                    static_cast<int8_t>(quant_one(xnew[j], row ? sv : sk));
+            }
+        }
+        if (threadIdx.x == 0) {
+            s_newscale[0] = sk;
+            s_newscale[1] = sv;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            int4 kk1[1], vv1[1];
+            kk1[0] = *reinterpret_cast<const int4*>(&s_newq[0][ds * 4]);
+            vv1[0] = *reinterpret_cast<const int4*>(&s_newq[1][ds * 4]);
+            const float sk1[1] = {s_newscale[0]}, sv1[1] = {s_newscale[1]};
+            const int tnew = len - 1;
+            if (sgi == 0 && tg == 0) {  // one store of the token per kv head
+                *reinterpret_cast<int4*>(a.k + (row0 + tnew) * D + ds * 16) = kk1[0];
+                *reinterpret_cast<int4*>(a.v + (row0 + tnew) * D + ds * 16) = vv1[0];
+                if (ds == 0) {
+                    a.ks[row0 + tnew] = sk1[0];
+                    a.vs[row0 + tnew] = sv1[0];
+                }
+            }
+            const bool ok1[1] = {tg == 0};
+            attend<SG, 1, LPT>(qr, kk1, vv1, sk1, sv1, ok1, a.scale_log2, m, l, acc);
+        }
     }
 
     // Merge the lane groups of this wave (lanes that share ds).
@@ -300,31 +416,31 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
             a.out[(bhq0 + h) * D + dim] = A / L;
         } else {
             const size_t rec = (bhq0 + h) * a.splits + split;
-            a.part_acc[rec * D + dim] = A;
+            put_coherent(a.part_acc + rec * D + dim, A);
             if (dim == 0) {
-                a.part_ml[rec * 2] = M;
-                a.part_ml[rec * 2 + 1] = L;
+                put_coherent(a.part_ml + rec * 2, M);
+                put_coherent(a.part_ml + rec * 2 + 1, L);
             }
         }
     }
 
     if (nsplit > 1 && a.counters != nullptr) {
-        // Release this split's record, count arrivals; the last arrival merges.
-        __threadfence();
+        // Count arrivals once this split's record is complete; the last arrival merges.
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (threadIdx.x == 0) {
-            const int prev = atomicAdd(a.counters + unit, 1);
+            const int prev = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             s_last = (prev == nsplit - 1);
         }
         __syncthreads();
         if (s_last) {
-            __threadfence();
             for (int i = threadIdx.x; i < SG * D; i += blockDim.x) {
                 const int h = i / D;
                 const int dim = i - h * D;
                 a.out[(bhq0 + h) * D + dim] = merge_dim(a, bhq0 + h, dim, nsplit);
             }
-            if (threadIdx.x == 0) a.counters[unit] = 0;  // ready for the next launch
+            if (threadIdx.x == 0)  // ready for the next launch
+                __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -413,12 +529,22 @@ hipError_t launch_fast_d(const DecodeArgs& a, const DecodePlan& p, hipStream_t s
 
 }  // namespace
 
-int fast_tile_tokens(int d) {
+template <int SG>
+int tile_tokens_sg(int d) {
     switch (d) {
-        case 32: return FastGeom<32>::BSTEP;
-        case 64: return FastGeom<64>::BSTEP;
-        case 128: return FastGeom<128>::BSTEP;
-        case 256: return FastGeom<256>::BSTEP;
+        case 32: return FastGeom<32, SG>::BSTEP;
+        case 64: return FastGeom<64, SG>::BSTEP;
+        case 128: return FastGeom<128, SG>::BSTEP;
+        case 256: return FastGeom<256, SG>::BSTEP;
+        default: return 0;
+    }
+}
+
+int fast_tile_tokens(int d, int sg) {
+    switch (sg) {
+        case 1: return tile_tokens_sg<1>(d);
+        case 2: return tile_tokens_sg<2>(d);
+        case 4: return tile_tokens_sg<4>(d);
         default: return 0;
     }
 }

@@ -37,6 +37,7 @@ struct DecodePlan {
     int nsg;         // G / sg
     int splits;      // splits per sequence (grid dimension)
     int chunk;       // tokens per split
+    bool counters;   // last-arriving split merges (fast path with a zeroed counter prefix)
     size_t counter_bytes, ml_bytes, acc_bytes;  // workspace regions (0 when splits == 1)
 };
 
@@ -54,9 +55,9 @@ hipError_t launch_quantize_rows(const float* x, int64_t rows, int d, int8_t* q, 
                                 hipStream_t stream);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 
-// Tile geometry of the fast kernel for a head dim (tokens one workgroup
-// iteration covers); 0 when the fast kernel does not support d.
-int fast_tile_tokens(int d);
+// Tokens one workgroup iteration of the fast kernel covers for head dim d and
+// sg query heads per workgroup; 0 when the fast kernel does not support d.
+int fast_tile_tokens(int d, int sg);
 int fast_heads_per_group(int G);
 
 }  // namespace kvq

@@ -164,12 +164,11 @@ def test_misaligned_pointers_use_generic_path(o):
     k.copy_(up(p["k"]))
     v.copy_(up(p["v"]))
     out = torch.empty((B, Hq, d), device=_gpu.dev())
-    params = kvq.decode_params(up(p["q"]), k, v, up(p["ks"]), up(p["vs"]), out, max_seq_len=cap)
-    keep = (params,)
+    gq, gks, gvs = up(p["q"]), up(p["ks"]), up(p["vs"])  # keep alive across the launch
+    params = kvq.decode_params(gq, k, v, gks, gvs, out, max_seq_len=cap)
     ws = kvq.new_workspace(params)
     kvq.decode_launch(params, ws)
     torch.cuda.synchronize()
-    del keep
     want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"])
     assert_close(down(out), want, what="misaligned")
 
