@@ -30,10 +30,11 @@ constexpr size_t kCounterBytes = 256 * 1024;
 constexpr long kMaxCounters = static_cast<long>(kCounterBytes / sizeof(int));
 // Workgroups a decode launch aims for when it picks the split count itself:
 // 8 per CU on MI355X's 256 CUs.
-#ifndef KVQ_TARGET_WG
-#define KVQ_TARGET_WG 256
-#endif
-constexpr int kTargetWorkgroups = KVQ_TARGET_WG;
+// Workgroups a decode launch aims for when it picks the split count itself
+// (MI355X: 256 CUs).  An 8-wave VALU workgroup fills a CU's issue slots on its
+// own; two 4-wave MFMA workgroups share a CU.
+constexpr int kTargetWorkgroupsValu = 256;
+constexpr int kTargetWorkgroupsMfma = 512;
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -46,10 +47,22 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, i
                      int max_splits, bool fused) {
     DecodePlan p{};
     const int G = Hq / Hkv;
-    const int sg = kvq::fast_heads_per_group(G);
-    const int tile = kvq::fast_tile_tokens(d, sg);
-    p.fast = tile > 0 && aligned;
-    p.sg = p.fast ? sg : 1;
+    const int sg_m = kvq::mfma_heads_per_group(G, d);
+    const int sg_v = kvq::fast_heads_per_group(G);
+    int tile = 0;
+    if (aligned && sg_m > 0) {
+        p.kernel = kvq::Kernel::Mfma;
+        p.sg = sg_m;
+        tile = kvq::mfma_tile_tokens();
+    } else if (aligned && kvq::fast_tile_tokens(d, sg_v) > 0) {
+        p.kernel = kvq::Kernel::Valu;
+        p.sg = sg_v;
+        tile = kvq::fast_tile_tokens(d, sg_v);
+    } else {
+        p.kernel = kvq::Kernel::Generic;
+        p.sg = 1;
+    }
+    p.fast = p.kernel != kvq::Kernel::Generic;
     p.nsg = p.fast ? G / p.sg : G;
     const long units = p.fast ? static_cast<long>(B) * Hkv * p.nsg : static_cast<long>(B) * Hq;
     const int gran = p.fast ? tile : 64;
@@ -61,7 +74,8 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, i
         splits = std::min<long>(splits, std::max(max_splits, 1));
         chunk = static_cast<int>((max_len + splits - 1) / splits);
     } else {
-        splits = (kTargetWorkgroups + units - 1) / units;
+        const long target = p.kernel == kvq::Kernel::Mfma ? kTargetWorkgroupsMfma : kTargetWorkgroupsValu;
+        splits = (target + units - 1) / units;
         splits = std::min<long>(splits, (max_len + gran - 1) / gran);
         splits = std::max<long>(1, std::min<long>(splits, std::max(max_splits, 1)));
         chunk = static_cast<int>((max_len + splits - 1) / splits);

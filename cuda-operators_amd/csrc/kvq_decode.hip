@@ -32,6 +32,7 @@
 
 #include "kvq_device.hpp"
 #include "kvq_internal.hpp"
+#include "kvq_split.hpp"
 
 namespace kvq {
 namespace {
@@ -55,61 +56,6 @@ struct FastGeom {
     static constexpr int WSTEP = TPL * U;             // tokens per wave iteration
     static constexpr int BSTEP = WSTEP * kFastWaves;  // tokens per workgroup iteration
 };
-
-__device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
-    const int len = a.lengths ? a.lengths[b] : a.uniform_len;
-    return min(max(len, 0), a.max_len);
-}
-
-// U consecutive per-token scales (U in {1,2,4,8}); p is U*4-byte aligned when
-// the token index is a multiple of U (tiles start at multiples of U tokens).
-template <int U>
-__device__ __forceinline__ void load_scales(const float* p, float (&out)[U]) {
-    if constexpr (U % 4 == 0) {
-#pragma unroll
-        for (int i = 0; i < U; i += 4) {
-            const float4 x = *reinterpret_cast<const float4*>(p + i);
-            out[i] = x.x;
-            out[i + 1] = x.y;
-            out[i + 2] = x.z;
-            out[i + 3] = x.w;
-        }
-    } else if constexpr (U == 2) {
-        const float2 x = *reinterpret_cast<const float2*>(p);
-        out[0] = x.x;
-        out[1] = x.y;
-    } else {
-#pragma unroll
-        for (int i = 0; i < U; i++) out[i] = p[i];
-    }
-}
-
-// Partial records cross workgroups (and XCDs, whose L2s are not coherent with
-// each other) inside one launch.  They are written and read with agent-scope
-// relaxed atomics, i.e. device-coherent global_store/global_load sc1, so no
-// L2-wide writeback/invalidate fence is needed; the producer waits for its
-// stores to complete (s_waitcnt 0) before it bumps the arrival counter.
-__device__ __forceinline__ void put_coherent(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float get_coherent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Log-sum-exp merge of the nsplit partial records of output row bhq, element dim.
-__device__ float merge_dim(const DecodeArgs& a, size_t bhq, int dim, int nsplit) {
-    const float* ml = a.part_ml + bhq * a.splits * 2;
-    const float* acc = a.part_acc + bhq * a.splits * a.d;
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, get_coherent(ml + 2 * s));
-    float L = 0.0f, A = 0.0f;
-    for (int s = 0; s < nsplit; s++) {
-        const float w = fast_exp2(get_coherent(ml + 2 * s) - M);
-        L = fmaf(get_coherent(ml + 2 * s + 1), w, L);
-        A = fmaf(get_coherent(acc + static_cast<size_t>(s) * a.d + dim), w, A);
-    }
-    return A / L;
-}
 
 // Online-softmax update of one lane group's state with U tokens (one per load).
 template <int SG, int U, int LPT>
@@ -412,37 +358,9 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
             L = fmaf(s_ml[w][h][1], f, L);
             A = fmaf(s_acc[w][h][dim], f, A);
         }
-        if (nsplit == 1) {
-            a.out[(bhq0 + h) * D + dim] = A / L;
-        } else {
-            const size_t rec = (bhq0 + h) * a.splits + split;
-            put_coherent(a.part_acc + rec * D + dim, A);
-            if (dim == 0) {
-                put_coherent(a.part_ml + rec * 2, M);
-                put_coherent(a.part_ml + rec * 2 + 1, L);
-            }
-        }
+        store_result(a, bhq0 + h, dim, split, nsplit, M, L, A);
     }
-
-    if (nsplit > 1 && a.counters != nullptr) {
-        // Count arrivals once this split's record is complete; the last arrival merges.
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const int prev = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = (prev == nsplit - 1);
-        }
-        __syncthreads();
-        if (s_last) {
-            for (int i = threadIdx.x; i < SG * D; i += blockDim.x) {
-                const int h = i / D;
-                const int dim = i - h * D;
-                a.out[(bhq0 + h) * D + dim] = merge_dim(a, bhq0 + h, dim, nsplit);
-            }
-            if (threadIdx.x == 0)  // ready for the next launch
-                __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
+    finish_split(a, unit, bhq0, SG, nsplit, &s_last);
 }
 
 __global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a) {
@@ -562,7 +480,13 @@ hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream) {
 
 hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
     hipError_t err;
-    if (p.fast) {
+    if (p.kernel == Kernel::Mfma) {
+        err = launch_decode_mfma(a, p, stream);
+        if (err != hipSuccess) return err;
+        if (a.counters == nullptr && p.splits > 1) return launch_merge(a, stream);
+        return hipSuccess;
+    }
+    if (p.kernel == Kernel::Valu) {
         switch (a.d) {
             case 32: err = launch_fast_d<32>(a, p, stream); break;
             case 64: err = launch_fast_d<64>(a, p, stream); break;

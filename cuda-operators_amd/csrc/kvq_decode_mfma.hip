@@ -1,0 +1,436 @@
+// kvq_decode_mfma.hip -- grouped-query decode attention on gfx950 matrix cores.
+//
+// For G query heads sharing a kv head the per-token work is a small dense
+// contraction (QK: [G x 128] x [128 x T], PV: [G x T] x [T x 128]), so with
+// G = 4 or 8 it runs on MFMA instead of per-lane FMAs.  Same math and result
+// contract as decode_fast (the reference's cpu_reference per query head,
+// kv_cache/KV_int8_split_optimized.cu:385-437); head_dim 128.
+//
+// One workgroup (4 waves) per (sequence split, batch, kv head, group of G
+// query heads); each wave walks 32-token tiles with its own online-softmax
+// state, merged across waves through LDS at the end.  Per tile:
+//
+// * QK on v_mfma_i32_16x16x64_i8.  The int8 K rows go from memory straight
+//   into the A operand (lane l: token l%16, dims 16*(l/16) + [0,16) of each
+//   64-dim block); no dequantisation instruction touches K.  q is held as three
+//   balanced int8 limbs of a 22-bit fixed-point value per head (q*2^E rounded
+//   once, |error| <= 2^-23 * max|q|), one MFMA column block per limb; the int32
+//   products are exact, and dot = ((C0*2^16 + C1*2^8) + C2) * 2^-E.
+//   MFMA rows n = 0..15 all carry head n % G (duplicates are free).
+// * softmax: the running max m of s = (dot * k_scale) * softmax_scale * log2 e
+//   gives the denominator; the PV weights w = p * v_scale are formed as
+//   exp2(s + log2 v_scale - mv) with their own running max mv, so they stay in
+//   [0, 1] whatever the scale magnitudes, and the accumulator is rescaled by
+//   exp2(mv - m) once at the end.
+// * PV on v_mfma_f32_16x16x32_f16 computing O^T[dim, row] += V^T P: the
+//   weights (x 2^12) are split into f16 hi + lo rows (rows n < G.. hold hi,
+//   the next G rows lo), so the product keeps ~22 bits; int8 V is exact in f16.
+//   V tiles are staged in LDS (rows XOR-swizzled in 16-byte pieces, conflict
+//   free) and read back transposed with ds_read_b64_tr_b8: within each 16-lane
+//   group, lanes 2r and 2r+1 address the two 8-byte halves of row r and lane i
+//   receives byte i of each row -- 8 tokens of one dim, the A operand layout.
+//   The token order of a lane group's k-slots (4g..4g+3, 16+4g..16+4g+3)
+//   matches where the QK C layout left that lane's probabilities, so P needs
+//   no data movement.
+// * fused append: the new token is quantised by the whole workgroup before
+//   each wave's last tile (its fp32 loads were issued at kernel start) and
+//   substituted from LDS where the last tile reads token length-1.
+#include <math.h>
+
+#include "kvq_device.hpp"
+#include "kvq_internal.hpp"
+#include "kvq_split.hpp"
+
+namespace kvq {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+
+constexpr int kMWaves = 4;        // waves per workgroup
+constexpr int kMTile = 32;        // tokens per wave tile
+constexpr int kMD = 128;          // head dim
+constexpr float kPScale = 4096.0f;  // PV weights are formed in [0, 2^12] before the f16 split
+constexpr int kMBStep = kMTile * kMWaves;
+
+// 8 signed bytes -> 8 f16 (exact): bias each byte to unsigned, place it under
+// the f16 exponent of 1024 (0x64xx = 1024 + u), subtract 1152 = 1024 + 128.
+__device__ __forceinline__ f16x8 i8x8_to_f16(i32x2 v) {
+    const unsigned x0 = static_cast<unsigned>(v.x) ^ 0x80808080u;
+    const unsigned x1 = static_cast<unsigned>(v.y) ^ 0x80808080u;
+    const unsigned w0 = __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u);
+    const unsigned w1 = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u);
+    const unsigned w2 = __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u);
+    const unsigned w3 = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u);
+    const f16x2 bias = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+    const f16x2 h0 = __builtin_bit_cast(f16x2, w0) - bias;
+    const f16x2 h1 = __builtin_bit_cast(f16x2, w1) - bias;
+    const f16x2 h2 = __builtin_bit_cast(f16x2, w2) - bias;
+    const f16x2 h3 = __builtin_bit_cast(f16x2, w3) - bias;
+    return f16x8{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
+}
+
+__device__ __forceinline__ int pack_bytes(const int* b) {
+    return (b[0] & 0xff) | ((b[1] & 0xff) << 8) | ((b[2] & 0xff) << 16) |
+           static_cast<int>(static_cast<unsigned>(b[3] & 0xff) << 24);
+}
+
+template <int G>
+__global__ __launch_bounds__(kMWaves* kWave) void decode_mfma(const DecodeArgs a) {
+    static_assert(G == 4 || G == 8, "heads per workgroup");
+    constexpr int NT = kMWaves * kWave;
+    static_assert(NT == 2 * kMD, "the fused append gives one K or V element to each thread");
+    __shared__ __align__(16) int8_t s_v[kMWaves][2][kMTile * kMD];
+    __shared__ __align__(16) float s_acc[kMWaves][16][kMD];
+    __shared__ float s_ml[kMWaves][G][2];
+    __shared__ __align__(16) int8_t s_newq[2][kMD];
+    __shared__ float s_newscale[2];
+    __shared__ float s_amax[2][2];
+    __shared__ int s_last;
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int r = lane & 15;   // MFMA row / token-in-subtile index
+    const int g = lane >> 4;   // 16-lane group
+
+    const int units = a.B * a.Hkv * a.nsg;
+    const int split = blockIdx.x / units;
+    const int unit = blockIdx.x - split * units;
+    const int bh = unit / a.nsg;
+    const int sgi = unit - bh * a.nsg;
+    const int b = bh / a.Hkv;
+    const int kvh = bh - b * a.Hkv;
+    const int hq0 = kvh * a.G + sgi * G;
+    const size_t bhq0 = static_cast<size_t>(b) * a.Hq + hq0;
+    const int len = seq_len_of(a, b);
+    const int nsplit = (len + a.chunk - 1) / a.chunk;
+
+    if (len == 0) {
+        if (split == 0)
+            for (int i = threadIdx.x; i < G * kMD; i += blockDim.x) a.out[bhq0 * kMD + i] = 0.0f;
+        return;
+    }
+    if (split >= nsplit) return;
+
+    const int t0 = split * a.chunk;
+    const int tend = min(len, t0 + a.chunk);
+    const bool app = (a.k_new != nullptr) && (tend == len);
+    const int tnew = len - 1;
+    const size_t row0 = static_cast<size_t>(bh) * a.cap;
+
+    // Fused append, part 1: this thread's element of the new K (threads
+    // 0..127) or V (128..255) row, fetched early.
+    float xnew = 0.0f;
+    if (app) xnew = (threadIdx.x < kMD ? a.k_new : a.v_new)[static_cast<size_t>(bh) * kMD + (threadIdx.x & (kMD - 1))];
+
+    // q of head (r % G) as int8 limbs in the QK B operand layout:
+    // qb[j][limb] holds dims 64j + 16g + [0,16).
+    const int hrow = r % G;
+    float qv[32];
+    {
+        const float* qp = a.q + (bhq0 + hrow) * kMD + 16 * g;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+#pragma unroll
+            for (int i4 = 0; i4 < 4; i4++) {
+                const float4 x = *reinterpret_cast<const float4*>(qp + 64 * j + 4 * i4);
+                qv[16 * j + 4 * i4] = x.x;
+                qv[16 * j + 4 * i4 + 1] = x.y;
+                qv[16 * j + 4 * i4 + 2] = x.z;
+                qv[16 * j + 4 * i4 + 3] = x.w;
+            }
+        }
+    }
+    float qmax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) qmax = fmaxf(qmax, fabsf(qv[i]));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+    int qexp = 0;
+    frexpf(qmax, &qexp);  // qmax < 2^qexp
+    const int E = qmax > 0.0f ? min(max(22 - qexp, -100), 126) : 0;
+    const float qdeq = ldexpf(1.0f, -E);
+    i32x4 qb[2][3];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        int limb[3][16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int Q = static_cast<int>(__builtin_rintf(ldexpf(qv[16 * j + i], E)));
+            const int l2 = ((Q + 128) & 255) - 128;
+            const int Q1 = (Q - l2) >> 8;
+            const int l1 = ((Q1 + 128) & 255) - 128;
+            limb[0][i] = (Q1 - l1) >> 8;
+            limb[1][i] = l1;
+            limb[2][i] = l2;
+        }
+#pragma unroll
+        for (int lb = 0; lb < 3; lb++)
+            qb[j][lb] = i32x4{pack_bytes(&limb[lb][0]), pack_bytes(&limb[lb][4]), pack_bytes(&limb[lb][8]),
+                              pack_bytes(&limb[lb][12])};
+    }
+
+    // Online-softmax state for head hrow (identical in every lane of that row)
+    // and the PV accumulator: acc[c] holds O^T[16c + 4g + i][row r].
+    float m = -INFINITY, mv = -INFINITY, lsum = 0.0f;
+    f32x4 acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const bool lo_row = ((r / G) & 1) != 0;
+
+    const int8_t* kbase = a.k + row0 * kMD;
+    const int8_t* vbase = a.v + row0 * kMD;
+    const float* ksb = a.ks + row0;
+    const float* vsb = a.vs + row0;
+
+    // The transposed V reads: lanes 2rr + h2 of group g address row R(rr),
+    // half h2, of each 16-dim piece.
+    const int rr = (lane & 15) >> 1;
+    const int h2 = lane & 1;
+    const int vrow = rr < 4 ? 4 * g + rr : 16 + 4 * g + (rr - 4);
+
+    // Fused append, part 2 (whole workgroup): per-row max|x| (waves 0,1: K;
+    // 2,3: V), the scale, one element per thread -- same rule and bits as
+    // append_kernel.  The row lands in LDS for the final tile and in the cache
+    // for later steps.
+    auto append_part2 = [&]() {
+        const float am = wave_max(fabsf(xnew));
+        if (lane == 0) s_amax[wave >> 1][wave & 1] = am;
+        __syncthreads();
+        const int row = threadIdx.x / kMD;
+        const int col = threadIdx.x & (kMD - 1);
+        const float scale = quant_scale(fmaxf(s_amax[row][0], s_amax[row][1]));
+        const int qn = quant_one(xnew, scale);
+        s_newq[row][col] = static_cast<int8_t>(qn);
+        if (col == 0) s_newscale[row] = scale;
+        if (sgi == 0) {
+            (row ? a.v : a.k)[(row0 + tnew) * kMD + col] = static_cast<int8_t>(qn);
+            if (col == 0) (row ? a.vs : a.ks)[row0 + tnew] = scale;
+        }
+        __syncthreads();
+    };
+
+    // One tile's global data in registers: K sub-tiles (A operand of QK), the
+    // 32 V rows (16 bytes per lane) and the scales of tokens base+16s+4g+i.
+    struct Tile {
+        i32x4 ka[2][2];
+        int4 v[4];
+        float ks[2][4], vs[2][4];
+    };
+    auto load_tile = [&](Tile& T, int base) {
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int tc = min(base + 16 * s + r, tend - 1);
+            const int8_t* kr = kbase + static_cast<size_t>(tc) * kMD + 16 * g;
+            const int4 x0 = load16_stream(kr), x1 = load16_stream(kr + 64);
+            T.ka[s][0] = i32x4{x0.x, x0.y, x0.z, x0.w};
+            T.ka[s][1] = i32x4{x1.x, x1.y, x1.z, x1.w};
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int tc = min(base + 8 * c + (lane >> 3), tend - 1);
+            T.v[c] = load16_stream(vbase + static_cast<size_t>(tc) * kMD + 16 * (lane & 7));
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int t4 = base + 16 * s + 4 * g;
+            const bool vec = t4 + 3 < tend &&
+                             ((reinterpret_cast<uintptr_t>(ksb + t4) | reinterpret_cast<uintptr_t>(vsb + t4)) & 15) == 0;
+            if (vec) {
+                load_scales<4>(ksb + t4, T.ks[s]);
+                load_scales<4>(vsb + t4, T.vs[s]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int tc = min(t4 + i, tend - 1);
+                    T.ks[s][i] = ksb[tc];
+                    T.vs[s][i] = vsb[tc];
+                }
+            }
+        }
+    };
+    // The appended token replaces what the cache held at position len-1 (only
+    // the workgroup's final tile can contain it).
+    auto substitute_new = [&](Tile& T, int base) {
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            if (base + 16 * s + r == tnew) {
+                T.ka[s][0] = *reinterpret_cast<const i32x4*>(&s_newq[0][16 * g]);
+                T.ka[s][1] = *reinterpret_cast<const i32x4*>(&s_newq[0][64 + 16 * g]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (base + 16 * s + 4 * g + i == tnew) {
+                    T.ks[s][i] = s_newscale[0];
+                    T.vs[s][i] = s_newscale[1];
+                }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            if (base + 8 * c + (lane >> 3) == tnew) T.v[c] = *reinterpret_cast<const int4*>(&s_newq[1][16 * (lane & 7)]);
+    };
+    // V rows into an LDS tile buffer: 16-byte piece p of row rw is stored at
+    // piece p ^ (rw & 7), so the transposed reads of 8 rows hit 8 different
+    // bank groups.
+    auto stage_v = [&](const Tile& T, int8_t* vt) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int rw = 8 * c + (lane >> 3);
+            const int p = lane & 7;
+            *reinterpret_cast<int4*>(vt + rw * kMD + ((p ^ (rw & 7)) << 4)) = T.v[c];
+        }
+    };
+    auto compute = [&](const Tile& T, int base, const int8_t* vt) {
+        // QK: C[token 4g + i][row r] per sub-tile and limb.
+        i32x4 cq[2][3];
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+#pragma unroll
+            for (int lb = 0; lb < 3; lb++) {
+                i32x4 c = i32x4{0, 0, 0, 0};
+                c = __builtin_amdgcn_mfma_i32_16x16x64_i8(T.ka[s][0], qb[0][lb], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_i32_16x16x64_i8(T.ka[s][1], qb[1][lb], c, 0, 0, 0);
+                cq[s][lb] = c;
+            }
+        }
+        // Scores (log2 units) and PV weight exponents; k-slot order s*4 + i.
+        float sc[8], sv[8];
+        float mt = -INFINITY, mvt = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const bool ok = base + 16 * s + 4 * g + i < tend;
+                const float dot = ((static_cast<float>(cq[s][0][i]) * 65536.0f + static_cast<float>(cq[s][1][i]) * 256.0f) +
+                                   static_cast<float>(cq[s][2][i])) * qdeq;
+                const float x = ok ? (dot * T.ks[s][i]) * a.scale_log2 : -INFINITY;
+                const float y = x + __builtin_amdgcn_logf(T.vs[s][i]);
+                sc[4 * s + i] = x;
+                sv[4 * s + i] = y;
+                mt = fmaxf(mt, x);
+                mvt = fmaxf(mvt, y);
+            }
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        mvt = fmaxf(mvt, __shfl_xor(mvt, 16));
+        mvt = fmaxf(mvt, __shfl_xor(mvt, 32));
+        const float mn = fmaxf(m, mt);
+        const float ms = mn == -INFINITY ? 0.0f : mn;
+        const float alpha = fast_exp2(m - ms);
+        float ps = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) ps += fast_exp2(sc[k] - ms);
+        lsum = lsum * alpha + ps;
+        m = mn;
+        const float mvn = fmaxf(mv, mvt);
+        const float mvs = mvn == -INFINITY ? 0.0f : mvn;
+        const float beta = fast_exp2(mv - mvs);
+        mv = mvn;
+#pragma unroll
+        for (int c = 0; c < 8; c++) acc[c] *= beta;
+        // P^T as the PV B operand: row r takes the hi or lo f16 part.
+        f16x8 pb;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float w = fast_exp2(sv[k] - mvs) * kPScale;
+            const _Float16 hi = static_cast<_Float16>(w);
+            const _Float16 lo = static_cast<_Float16>(w - static_cast<float>(hi));
+            pb[k] = lo_row ? lo : hi;
+        }
+        // PV: 8 blocks of 16 dims.
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int8_t* src = vt + vrow * kMD + ((c ^ (vrow & 7)) << 4) + 8 * h2;
+            const i32x2 vb = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(const_cast<int8_t*>(src)));
+            acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_f16(vb), pb, acc[c], 0, 0, 0);
+        }
+    };
+
+    // Software-pipelined tile loop: tile i+1's global loads are in flight
+    // while tile i is computed (from registers and LDS buffer i % 2).  The
+    // fused append runs before each wave's last tile (a workgroup barrier, so
+    // waves without tiles join it too).
+    const int wbase = t0 + wave * kMTile;
+    const int ntiles = wbase < tend ? (tend - wbase + kMBStep - 1) / kMBStep : 0;
+    Tile cur, nxt;
+    if (ntiles > 0) load_tile(cur, wbase);
+    for (int it = 0; it < ntiles; it++) {
+        const int base = wbase + it * kMBStep;
+        const bool last = it + 1 == ntiles;
+        if (!last) load_tile(nxt, base + kMBStep);
+        if (last && app) {
+            append_part2();
+            substitute_new(cur, base);
+        }
+        int8_t* vt = s_v[wave][it & 1];
+        stage_v(cur, vt);
+        compute(cur, base, vt);
+        if (!last) cur = nxt;
+    }
+    if (ntiles == 0 && app) append_part2();
+
+
+    // Wave results to LDS: the softmax sum over the 4 lane groups, and the
+    // accumulator rescaled from the weight max mv to the score max m.
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    const float fct = (m == -INFINITY || mv == -INFINITY) ? 0.0f : fast_exp2(mv - m) * (1.0f / kPScale);
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) s_acc[wave][r][16 * c + 4 * g + i] = acc[c][i] * fct;
+    }
+    if (g == 0 && r < G) {
+        s_ml[wave][r][0] = m;
+        s_ml[wave][r][1] = lsum;
+    }
+    __syncthreads();
+
+    // Merge the waves and the hi/lo rows; one thread per (head, element).
+    for (int i = threadIdx.x; i < G * kMD; i += blockDim.x) {
+        const int h = i / kMD;
+        const int dim = i - h * kMD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kMWaves; w++) M = fmaxf(M, s_ml[w][h][0]);
+        const float Ms = M == -INFINITY ? 0.0f : M;
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kMWaves; w++) {
+            const float f = fast_exp2(s_ml[w][h][0] - Ms);
+            L = fmaf(s_ml[w][h][1], f, L);
+            A = fmaf(s_acc[w][h][dim] + s_acc[w][h + G][dim], f, A);
+        }
+        store_result(a, bhq0 + h, dim, split, nsplit, M, L, A);
+    }
+    finish_split(a, unit, bhq0, G, nsplit, &s_last);
+}
+
+}  // namespace
+
+int mfma_tile_tokens() { return kMBStep; }
+
+int mfma_heads_per_group(int G, int d) {
+    if (d != kMD) return 0;
+    if (G % 8 == 0) return 8;
+    if (G % 4 == 0) return 4;
+    return 0;
+}
+
+hipError_t launch_decode_mfma(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(a.B * a.Hkv * p.nsg * p.splits));
+    const dim3 block(kMWaves * kWave);
+    switch (p.sg) {
+        case 4: hipLaunchKernelGGL(decode_mfma<4>, grid, block, 0, stream, a); break;
+        case 8: hipLaunchKernelGGL(decode_mfma<8>, grid, block, 0, stream, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace kvq

@@ -30,10 +30,18 @@ struct DecodeArgs {
     float scale_log2;        // softmax_scale * log2(e)
 };
 
+// Which decode kernel a plan runs.
+enum class Kernel {
+    Generic,  // any head dim / alignment (decode_generic)
+    Valu,     // decode_fast: d in {32,64,128,256}, per-lane FMAs
+    Mfma,     // decode_mfma: d = 128, 4 or 8 query heads per kv head group
+};
+
 // Launch plan chosen on the host.
 struct DecodePlan {
-    bool fast;       // tuned kernel (d in {32,64,128,256}, 16-byte aligned rows)
-    int sg;          // query heads per workgroup (fast path)
+    Kernel kernel;
+    bool fast;       // a tuned kernel (Valu or Mfma): 16-byte aligned rows
+    int sg;          // query heads per workgroup (tuned kernels)
     int nsg;         // G / sg
     int splits;      // splits per sequence (grid dimension)
     int chunk;       // tokens per split
@@ -59,5 +67,10 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 // sg query heads per workgroup; 0 when the fast kernel does not support d.
 int fast_tile_tokens(int d, int sg);
 int fast_heads_per_group(int G);
+// decode_mfma: query heads per workgroup for group size G and head dim d (0:
+// not applicable), tokens per workgroup iteration, launcher.
+int mfma_heads_per_group(int G, int d);
+int mfma_tile_tokens();
+hipError_t launch_decode_mfma(const DecodeArgs& a, const DecodePlan& plan, hipStream_t stream);
 
 }  // namespace kvq

@@ -80,7 +80,7 @@ def test_split_counts_agree(o, splits):
     assert_close(got, want, what=f"splits={splits}")
 
 
-@pytest.mark.parametrize("G", [1, 2, 3, 4, 6, 8, 16])
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 6, 8, 12, 16])
 @pytest.mark.parametrize("d", [64, 128])
 def test_group_sizes(o, G, d):
     """Query heads per kv head: 1 (MHA) .. 16, incl. groups the kernel tiles as 4+4 or 1+1+1."""
@@ -125,13 +125,14 @@ def test_softmax_scale_override(o):
     assert_close(got, want, what="softmax_scale")
 
 
-@pytest.mark.parametrize("d", [64, 128, 256, 96])
-def test_fused_append_matches_separate_append(o, d):
+@pytest.mark.parametrize("d,G", [(64, 2), (128, 2), (256, 2), (96, 2), (128, 4), (128, 8), (128, 16)])
+def test_fused_append_matches_separate_append(o, d, G):
     """Fused append inside the decode kernel == kvq_append_launch followed by decode:
     bit-for-bit in the cache; the outputs agree to fp32 rounding (the new token
     enters the online softmax at a different point of the summation order)."""
-    rng = np.random.default_rng(d)
-    B, Hq, Hkv, cap = 3, 8, 4, 700
+    rng = np.random.default_rng(d + G)
+    B, Hkv, cap = 3, 2, 700
+    Hq = Hkv * G
     lengths = np.array([700, 1, 389], np.int32)
     p = make_problem(rng, B, Hq, Hkv, cap, d, o.quantize_rows, lengths=lengths)
     kn = rng.standard_normal((B, Hkv, d), dtype=np.float32) * np.float32(3)
@@ -148,7 +149,7 @@ def test_fused_append_matches_separate_append(o, d):
     o.append(kn, vn, p["k"], p["v"], p["ks"], p["vs"], positions=lengths - 1)
     assert np.array_equal(fused[1], p["k"]) and np.array_equal(_bits(fused[3]), _bits(p["ks"]))
     want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
-    assert_close(fused[0], want, what=f"fused append d={d}")
+    assert_close(fused[0], want, what=f"fused append d={d} G={G}")
 
 
 def test_misaligned_pointers_use_generic_path(o):
@@ -198,3 +199,37 @@ def test_side_stream(o):
     with torch.cuda.stream(s):
         got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], stream=s)[0]
     assert_close(got, o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"]), what="side stream")
+
+
+@pytest.mark.parametrize("splits", [1, 3, 8])
+@pytest.mark.parametrize("G", [4, 8])
+def test_mfma_splits_with_fused_append(o, G, splits):
+    """Grouped-query (matrix-core) path: fused append in the last split, split merge."""
+    rng = np.random.default_rng(100 * G + splits)
+    B, Hkv, cap, d = 3, 2, 1500, 128
+    lengths = np.array([1500, 33, 1025], np.int32)
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, dist="student_t", lengths=lengths)
+    kn = rng.standard_t(4, (B, Hkv, d)).astype(np.float32)
+    vn = rng.standard_t(4, (B, Hkv, d)).astype(np.float32)
+    got, gk, gv, gks, gvs = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths, splits=splits,
+                                         k_new=kn, v_new=vn)
+    o.append(kn, vn, p["k"], p["v"], p["ks"], p["vs"], positions=lengths - 1)
+    assert np.array_equal(gk, p["k"]) and np.array_equal(gv, p["v"])
+    assert np.array_equal(_bits(gks), _bits(p["ks"])) and np.array_equal(_bits(gvs), _bits(p["vs"]))
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert_close(got, want, what=f"mfma G={G} splits={splits}")
+
+
+def test_mfma_extreme_scales(o):
+    """Tiny, huge and zero per-token scales and a large |q| on the matrix-core path."""
+    rng = np.random.default_rng(77)
+    B, Hkv, G, cap, d = 1, 2, 8, 300, 128
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows)
+    p["vs"][0, 0, :50] = np.float32(1e-30)
+    p["vs"][0, 0, 50:60] = np.float32(0.0)
+    p["vs"][0, 1, :40] = np.float32(3e4)
+    p["ks"][0, 1, 100:120] = np.float32(1e-6)
+    p["q"][0, 3] *= np.float32(50.0)
+    got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"])[0]
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"])
+    assert_close(got, want, what="mfma extreme scales")
