@@ -87,8 +87,10 @@ __device__ __forceinline__ void attend(const float (&qr)[SG][16], const int4 (&k
         const float ms = (mx == -INFINITY) ? 0.0f : mx;
         const float alpha = fast_exp2(m[h] - ms);
         l[h] *= alpha;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {  // the max moved in some lane group
 #pragma unroll
-        for (int j = 0; j < 16; j++) acc[h][j] *= alpha;
+            for (int j = 0; j < 16; j++) acc[h][j] *= alpha;
+        }
         m[h] = mx;
 #pragma unroll
         for (int u = 0; u < U; u++) {

@@ -80,7 +80,8 @@ __device__ __forceinline__ int pack_bytes(const int* b) {
 }
 
 template <int G>
-__global__ __launch_bounds__(kMWaves* kWave) void decode_mfma(const DecodeArgs a) {
+__global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma(
+    const DecodeArgs a) {
     static_assert(G == 4 || G == 8, "heads per workgroup");
     constexpr int NT = kMWaves * kWave;
     static_assert(NT == 2 * kMD, "the fused append gives one K or V element to each thread");
@@ -224,16 +225,16 @@ __global__ __launch_bounds__(kMWaves* kWave) void decode_mfma(const DecodeArgs a
     auto load_tile = [&](Tile& T, int base) {
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            const int tc = min(base + 16 * s + r, tend - 1);
-            const int8_t* kr = kbase + static_cast<size_t>(tc) * kMD + 16 * g;
+            const unsigned tc = min(base + 16 * s + r, tend - 1);
+            const int8_t* kr = kbase + (tc * kMD + 16 * g);
             const int4 x0 = load16_stream(kr), x1 = load16_stream(kr + 64);
             T.ka[s][0] = i32x4{x0.x, x0.y, x0.z, x0.w};
             T.ka[s][1] = i32x4{x1.x, x1.y, x1.z, x1.w};
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const int tc = min(base + 8 * c + (lane >> 3), tend - 1);
-            T.v[c] = load16_stream(vbase + static_cast<size_t>(tc) * kMD + 16 * (lane & 7));
+            const unsigned tc = min(base + 8 * c + (lane >> 3), tend - 1);
+            T.v[c] = load16_stream(vbase + (tc * kMD + 16 * (lane & 7)));
         }
 #pragma unroll
         for (int s = 0; s < 2; s++) {
@@ -331,8 +332,10 @@ __global__ __launch_bounds__(kMWaves* kWave) void decode_mfma(const DecodeArgs a
         const float mvs = mvn == -INFINITY ? 0.0f : mvn;
         const float beta = fast_exp2(mv - mvs);
         mv = mvn;
+        if (__builtin_amdgcn_ballot_w64(beta != 1.0f) != 0) {  // the max moved in some row
 #pragma unroll
-        for (int c = 0; c < 8; c++) acc[c] *= beta;
+            for (int c = 0; c < 8; c++) acc[c] *= beta;
+        }
         // P^T as the PV B operand: row r takes the hi or lo f16 part.
         f16x8 pb;
 #pragma unroll
