@@ -90,8 +90,8 @@ def cpu_baseline(prob, budget_s):
         "unit": "GB/s",
         "cores": o.threads,
         "kind": "port",
-        "sample": (f"full {prob.name} step (append + decode, {prob.B}x{prob.Hq} heads), "
-                   f"median of {len(times)} runs: {t * 1e6:.0f} us/step"),
+        "sample": (f"full {prob.name} step ({'append + ' if kn is not None else ''}decode, "
+                   f"{prob.B}x{prob.Hq} query heads), median of {len(times)} runs: {t * 1e6:.0f} us/step"),
     }
 
 

@@ -222,7 +222,48 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         int4 v[4];
         float ks[2][4], vs[2][4];
     };
-    auto load_tile = [&](Tile& T, int base) {
+    const int wbase = t0 + wave * kMTile;
+    const int ntiles = wbase < tend ? (tend - wbase + kMBStep - 1) / kMBStep : 0;
+    // Lane pointers for tile base `wbase`; a full tile advances them by a
+    // constant, only a tile reaching past tend clamps per token.
+    const int8_t* kp0 = kbase + (static_cast<unsigned>(wbase + r) * kMD + 16 * g);
+    const int8_t* vp0 = vbase + (static_cast<unsigned>(wbase + (lane >> 3)) * kMD + 16 * (lane & 7));
+    const float* ksp0 = ksb + (wbase + 4 * g);
+    const float* vsp0 = vsb + (wbase + 4 * g);
+    const bool scales_vec = ((reinterpret_cast<uintptr_t>(ksp0) | reinterpret_cast<uintptr_t>(vsp0)) & 15) == 0;
+    auto load_tile = [&](Tile& T, int it) {
+        const int base = wbase + it * kMBStep;
+        if (base + kMTile <= tend) {
+            const int8_t* kp = kp0 + static_cast<size_t>(it) * (kMBStep * kMD);
+            const int8_t* vp = vp0 + static_cast<size_t>(it) * (kMBStep * kMD);
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const int4 x0 = load16_stream(kp + s * 16 * kMD), x1 = load16_stream(kp + s * 16 * kMD + 64);
+                T.ka[s][0] = i32x4{x0.x, x0.y, x0.z, x0.w};
+                T.ka[s][1] = i32x4{x1.x, x1.y, x1.z, x1.w};
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) T.v[c] = load16_stream(vp + c * 8 * kMD);
+            const float* ksp = ksp0 + it * kMBStep;
+            const float* vsp = vsp0 + it * kMBStep;
+            if (scales_vec) {
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
+                    load_scales<4>(ksp + 16 * s, T.ks[s]);
+                    load_scales<4>(vsp + 16 * s, T.vs[s]);
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < 2; s++) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        T.ks[s][i] = ksp[16 * s + i];
+                        T.vs[s][i] = vsp[16 * s + i];
+                    }
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             const unsigned tc = min(base + 16 * s + r, tend - 1);
@@ -238,19 +279,11 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         }
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            const int t4 = base + 16 * s + 4 * g;
-            const bool vec = t4 + 3 < tend &&
-                             ((reinterpret_cast<uintptr_t>(ksb + t4) | reinterpret_cast<uintptr_t>(vsb + t4)) & 15) == 0;
-            if (vec) {
-                load_scales<4>(ksb + t4, T.ks[s]);
-                load_scales<4>(vsb + t4, T.vs[s]);
-            } else {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int tc = min(t4 + i, tend - 1);
-                    T.ks[s][i] = ksb[tc];
-                    T.vs[s][i] = vsb[tc];
-                }
+            for (int i = 0; i < 4; i++) {
+                const int tc = min(base + 16 * s + 4 * g + i, tend - 1);
+                T.ks[s][i] = ksb[tc];
+                T.vs[s][i] = vsb[tc];
             }
         }
     };
@@ -358,14 +391,12 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // while tile i is computed (from registers and LDS buffer i % 2).  The
     // fused append runs before each wave's last tile (a workgroup barrier, so
     // waves without tiles join it too).
-    const int wbase = t0 + wave * kMTile;
-    const int ntiles = wbase < tend ? (tend - wbase + kMBStep - 1) / kMBStep : 0;
     Tile cur, nxt;
-    if (ntiles > 0) load_tile(cur, wbase);
+    if (ntiles > 0) load_tile(cur, 0);
     for (int it = 0; it < ntiles; it++) {
         const int base = wbase + it * kMBStep;
         const bool last = it + 1 == ntiles;
-        if (!last) load_tile(nxt, base + kMBStep);
+        if (!last) load_tile(nxt, it + 1);
         if (last && app) {
             append_part2();
             substitute_new(cur, base);
