@@ -41,16 +41,19 @@ size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Split count and workspace layout for one decode problem.
+// aligned: q, caches and new rows are 16-byte aligned (vector loads);
+// quads: the matrix-core kernel may load 4 consecutive scales as one float4
+// (scale arrays 16-byte aligned, capacity a multiple of 4);
 // max_splits bounds the splits (scratch capacity of the reference ABI);
 // fused selects the arrival-counter merge (workspace holds counters).
-DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, int requested,
+DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, bool quads, int requested,
                      int max_splits, bool fused) {
     DecodePlan p{};
     const int G = Hq / Hkv;
     const int sg_m = kvq::mfma_heads_per_group(G, d);
     const int sg_v = kvq::fast_heads_per_group(G);
     int tile = 0;
-    if (aligned && sg_m > 0) {
+    if (aligned && quads && sg_m > 0) {
         p.kernel = kvq::Kernel::Mfma;
         p.sg = sg_m;
         tile = kvq::mfma_tile_tokens();
@@ -73,6 +76,8 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, i
         splits = std::min<long>(requested, max_len);
         splits = std::min<long>(splits, std::max(max_splits, 1));
         chunk = static_cast<int>((max_len + splits - 1) / splits);
+        // Matrix-core tiles start at multiples of 4 tokens (aligned scale quads).
+        if (p.kernel == kvq::Kernel::Mfma && splits > 1) chunk = static_cast<int>(round_up(static_cast<size_t>(chunk), 4));
     } else {
         const long target = p.kernel == kvq::Kernel::Mfma ? kTargetWorkgroupsMfma : kTargetWorkgroupsValu;
         splits = (target + units - 1) / units;
@@ -140,7 +145,7 @@ hipError_t reference_launch(const float* Q, const int8_t* K, const int8_t* V, co
     DecodeArgs a = reference_args(Q, K, V, ks, vs, out, H, N, d);
     // S holds H*N floats; a split needs (d + 2) floats per head.
     const int max_splits = std::max(1, N / (d + 2));
-    const DecodePlan p = make_plan(1, H, H, d, N, reference_aligned(Q, K, V, d), 0, max_splits, false);
+    const DecodePlan p = make_plan(1, H, H, d, N, reference_aligned(Q, K, V, d), false, 0, max_splits, false);
     a.splits = p.splits;
     a.chunk = p.chunk;
     a.nsg = p.nsg;
@@ -207,9 +212,13 @@ bool decode_aligned(const kvq_decode_params* p) {
            (!p->k_new || (aligned16(p->k_new) && aligned16(p->v_new)));
 }
 
+bool decode_scale_quads(const kvq_decode_params* p) {
+    return aligned16(p->k_scale) && aligned16(p->v_scale) && (p->capacity % 4) == 0;
+}
+
 DecodePlan decode_plan(const kvq_decode_params* p) {
     return make_plan(p->batch, p->num_q_heads, p->num_kv_heads, p->head_dim, decode_max_len(p),
-                     decode_aligned(p), p->num_splits, INT_MAX, true);
+                     decode_aligned(p), decode_scale_quads(p), p->num_splits, INT_MAX, true);
 }
 
 }  // namespace
@@ -231,7 +240,7 @@ void solve(const float* Q, const int8_t* K_int8, const int8_t* V_int8, const flo
     }
     DecodeArgs a = reference_args(Q, K_int8, V_int8, k_scale, v_scale, output, num_heads, seq_len, head_dim);
     const DecodePlan p = make_plan(1, num_heads, num_heads, head_dim, seq_len,
-                                   reference_aligned(Q, K_int8, V_int8, head_dim), 0, INT_MAX, true);
+                                   reference_aligned(Q, K_int8, V_int8, head_dim), false, 0, INT_MAX, true);
     a.splits = p.splits;
     a.chunk = p.chunk;
     a.nsg = p.nsg;

@@ -18,13 +18,13 @@
 //   products are exact, and dot = ((C0*2^16 + C1*2^8) + C2) * 2^-E.
 //   MFMA rows n = 0..15 all carry head n % G (duplicates are free).
 // * softmax: the running max m of s = (dot * k_scale) * softmax_scale * log2 e
-//   gives the denominator; the PV weights w = p * v_scale are formed as
-//   exp2(s + log2 v_scale - mv) with their own running max mv, so they stay in
-//   [0, 1] whatever the scale magnitudes, and the accumulator is rescaled by
-//   exp2(mv - m) once at the end.
+//   gives p = exp2(s - m) and the denominator; the PV weights are
+//   w = p * v_scale * 2^15 / vref, with vref the running max of |v_scale|, so
+//   |w| <= 2^15 whatever the scale magnitudes.  A tile that raises m or vref
+//   rescales the accumulator once (skipped when no row of the wave changed).
 // * PV on v_mfma_f32_16x16x32_f16 computing O^T[dim, row] += V^T P: the
-//   weights (x 2^12) are split into f16 hi + lo rows (rows n < G.. hold hi,
-//   the next G rows lo), so the product keeps ~22 bits; int8 V is exact in f16.
+//   weights are split into f16 hi + lo rows (rows n < G.. hold hi, the next G
+//   rows lo), so the product keeps ~22 bits; int8 V is exact in f16.
 //   V tiles are staged in LDS (rows XOR-swizzled in 16-byte pieces, conflict
 //   free) and read back transposed with ds_read_b64_tr_b8: within each 16-lane
 //   group, lanes 2r and 2r+1 address the two 8-byte halves of row r and lane i
@@ -54,7 +54,7 @@ typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 constexpr int kMWaves = 4;        // waves per workgroup
 constexpr int kMTile = 32;        // tokens per wave tile
 constexpr int kMD = 128;          // head dim
-constexpr float kPScale = 4096.0f;  // PV weights are formed in [0, 2^12] before the f16 split
+constexpr float kPScale = 32768.0f;  // PV weights are formed in [-2^15, 2^15] before the f16 split
 constexpr int kMBStep = kMTile * kMWaves;
 
 // 8 signed bytes -> 8 f16 (exact): bias each byte to unsigned, place it under
@@ -175,13 +175,17 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
                               pack_bytes(&limb[lb][12])};
     }
 
-    // Online-softmax state for head hrow (identical in every lane of that row)
-    // and the PV accumulator: acc[c] holds O^T[16c + 4g + i][row r].
-    float m = -INFINITY, mv = -INFINITY, lsum = 0.0f;
+    // Online-softmax state of head hrow (identical in every lane of that
+    // row): the score max m (log2 units), the denominator lsum, and vref, the
+    // running max of |v_scale| that keeps the PV weights p * v_scale / vref in
+    // [-1, 1].  acc[c] holds O^T[16c + 4g + i][row r] in units of
+    // vref / kPScale.
+    float m = -INFINITY, lsum = 0.0f, vref = 0.0f;
     f32x4 acc[8];
 #pragma unroll
     for (int c = 0; c < 8; c++) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const bool lo_row = ((r / G) & 1) != 0;
+    const float qs = qdeq * a.scale_log2;  // integer dot -> score in log2 units (after x k_scale)
 
     const int8_t* kbase = a.k + row0 * kMD;
     const int8_t* vbase = a.v + row0 * kMD;
@@ -225,12 +229,12 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     const int wbase = t0 + wave * kMTile;
     const int ntiles = wbase < tend ? (tend - wbase + kMBStep - 1) / kMBStep : 0;
     // Lane pointers for tile base `wbase`; a full tile advances them by a
-    // constant, only a tile reaching past tend clamps per token.
+    // constant (the host guarantees 16-byte aligned scale quads), only a tile
+    // reaching past tend clamps per token.
     const int8_t* kp0 = kbase + (static_cast<unsigned>(wbase + r) * kMD + 16 * g);
     const int8_t* vp0 = vbase + (static_cast<unsigned>(wbase + (lane >> 3)) * kMD + 16 * (lane & 7));
     const float* ksp0 = ksb + (wbase + 4 * g);
     const float* vsp0 = vsb + (wbase + 4 * g);
-    const bool scales_vec = ((reinterpret_cast<uintptr_t>(ksp0) | reinterpret_cast<uintptr_t>(vsp0)) & 15) == 0;
     auto load_tile = [&](Tile& T, int it) {
         const int base = wbase + it * kMBStep;
         if (base + kMTile <= tend) {
@@ -244,23 +248,10 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             }
 #pragma unroll
             for (int c = 0; c < 4; c++) T.v[c] = load16_stream(vp + c * 8 * kMD);
-            const float* ksp = ksp0 + it * kMBStep;
-            const float* vsp = vsp0 + it * kMBStep;
-            if (scales_vec) {
 #pragma unroll
-                for (int s = 0; s < 2; s++) {
-                    load_scales<4>(ksp + 16 * s, T.ks[s]);
-                    load_scales<4>(vsp + 16 * s, T.vs[s]);
-                }
-            } else {
-#pragma unroll
-                for (int s = 0; s < 2; s++) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        T.ks[s][i] = ksp[16 * s + i];
-                        T.vs[s][i] = vsp[16 * s + i];
-                    }
-                }
+            for (int s = 0; s < 2; s++) {
+                load_scales<4>(ksp0 + it * kMBStep + 16 * s, T.ks[s]);
+                load_scales<4>(vsp0 + it * kMBStep + 16 * s, T.vs[s]);
             }
             return;
         }
@@ -287,9 +278,21 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             }
         }
     };
+    // V rows into an LDS tile buffer: 16-byte piece p of row rw is stored at
+    // piece p ^ (rw & 7), so the transposed reads of 8 rows hit 8 different
+    // bank groups.
+    auto stage_v = [&](const Tile& T, int8_t* vt) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int rw = 8 * c + (lane >> 3);
+            const int p = lane & 7;
+            *reinterpret_cast<int4*>(vt + rw * kMD + ((p ^ (rw & 7)) << 4)) = T.v[c];
+        }
+    };
     // The appended token replaces what the cache held at position len-1 (only
-    // the workgroup's final tile can contain it).
-    auto substitute_new = [&](Tile& T, int base) {
+    // the workgroup's final tile can contain it): K and scales in registers,
+    // the V row in the tile's LDS buffer.
+    auto substitute_new = [&](Tile& T, int base, int8_t* vt) {
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             if (base + 16 * s + r == tnew) {
@@ -303,20 +306,10 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
                     T.vs[s][i] = s_newscale[1];
                 }
         }
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-            if (base + 8 * c + (lane >> 3) == tnew) T.v[c] = *reinterpret_cast<const int4*>(&s_newq[1][16 * (lane & 7)]);
-    };
-    // V rows into an LDS tile buffer: 16-byte piece p of row rw is stored at
-    // piece p ^ (rw & 7), so the transposed reads of 8 rows hit 8 different
-    // bank groups.
-    auto stage_v = [&](const Tile& T, int8_t* vt) {
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int rw = 8 * c + (lane >> 3);
-            const int p = lane & 7;
-            *reinterpret_cast<int4*>(vt + rw * kMD + ((p ^ (rw & 7)) << 4)) = T.v[c];
-        }
+        const int rw = tnew - base;
+        if (rw >= 0 && rw < kMTile && lane < 8)
+            *reinterpret_cast<int4*>(vt + rw * kMD + ((lane ^ (rw & 7)) << 4)) =
+                *reinterpret_cast<const int4*>(&s_newq[1][16 * lane]);
     };
     auto compute = [&](const Tile& T, int base, const int8_t* vt) {
         // QK: C[token 4g + i][row r] per sub-tile and limb.
@@ -331,53 +324,61 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
                 cq[s][lb] = c;
             }
         }
-        // Scores (log2 units) and PV weight exponents; k-slot order s*4 + i.
-        float sc[8], sv[8];
-        float mt = -INFINITY, mvt = -INFINITY;
+        // Scores in log2 units, k-slot order s*4 + i: the low limbs combine
+        // exactly in int32 ((C1 << 8) + C2 < 2^30), the top limb in fp32.
+        float sc[8];
+        float mt = -INFINITY, vmax = 0.0f;
 #pragma unroll
         for (int s = 0; s < 2; s++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const bool ok = base + 16 * s + 4 * g + i < tend;
-                const float dot = ((static_cast<float>(cq[s][0][i]) * 65536.0f + static_cast<float>(cq[s][1][i]) * 256.0f) +
-                                   static_cast<float>(cq[s][2][i])) * qdeq;
-                const float x = ok ? (dot * T.ks[s][i]) * a.scale_log2 : -INFINITY;
-                const float y = x + __builtin_amdgcn_logf(T.vs[s][i]);
-                sc[4 * s + i] = x;
-                sv[4 * s + i] = y;
-                mt = fmaxf(mt, x);
-                mvt = fmaxf(mvt, y);
+                const int low = (cq[s][1][i] << 8) + cq[s][2][i];
+                const float dot = static_cast<float>(cq[s][0][i]) * 65536.0f + static_cast<float>(low);
+                sc[4 * s + i] = (dot * T.ks[s][i]) * qs;
+                vmax = fmaxf(vmax, fabsf(T.vs[s][i]));
             }
         }
+        if (base + kMTile > tend) {  // tail tile: tokens past tend do not count
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (base + 16 * s + 4 * g + i >= tend) sc[4 * s + i] = -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) mt = fmaxf(mt, sc[k]);
         mt = fmaxf(mt, __shfl_xor(mt, 16));
         mt = fmaxf(mt, __shfl_xor(mt, 32));
-        mvt = fmaxf(mvt, __shfl_xor(mvt, 16));
-        mvt = fmaxf(mvt, __shfl_xor(mvt, 32));
+        vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
+        vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
         const float mn = fmaxf(m, mt);
         const float ms = mn == -INFINITY ? 0.0f : mn;
         const float alpha = fast_exp2(m - ms);
-        float ps = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; k++) ps += fast_exp2(sc[k] - ms);
-        lsum = lsum * alpha + ps;
+        const float vn = fmaxf(vref, vmax);
+        const float rvn = vn > 0.0f ? __builtin_amdgcn_rcpf(vn) : 0.0f;  // v_rcp_f32, 1 ulp
+        const float f = vn > 0.0f ? alpha * (vref * rvn) : alpha;
+        const float winv = kPScale * rvn;
         m = mn;
-        const float mvn = fmaxf(mv, mvt);
-        const float mvs = mvn == -INFINITY ? 0.0f : mvn;
-        const float beta = fast_exp2(mv - mvs);
-        mv = mvn;
-        if (__builtin_amdgcn_ballot_w64(beta != 1.0f) != 0) {  // the max moved in some row
+        vref = vn;
+        if (__builtin_amdgcn_ballot_w64(f != 1.0f) != 0) {  // a row's max or vref moved
 #pragma unroll
-            for (int c = 0; c < 8; c++) acc[c] *= beta;
+            for (int c = 0; c < 8; c++) acc[c] *= f;
         }
-        // P^T as the PV B operand: row r takes the hi or lo f16 part.
+        // P^T as the PV B operand: row r takes the hi or lo f16 part of
+        // w = p * v_scale * kPScale / vref.
+        float ps = 0.0f;
         f16x8 pb;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const float w = fast_exp2(sv[k] - mvs) * kPScale;
+            const float p = fast_exp2(sc[k] - ms);
+            ps += p;
+            const float w = p * (T.vs[k >> 2][k & 3] * winv);
             const _Float16 hi = static_cast<_Float16>(w);
             const _Float16 lo = static_cast<_Float16>(w - static_cast<float>(hi));
             pb[k] = lo_row ? lo : hi;
         }
+        lsum = lsum * alpha + ps;
         // PV: 8 blocks of 16 dims.
 #pragma unroll
         for (int c = 0; c < 8; c++) {
@@ -388,32 +389,36 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     };
 
     // Software-pipelined tile loop: tile i+1's global loads are in flight
-    // while tile i is computed (from registers and LDS buffer i % 2).  The
-    // fused append runs before each wave's last tile (a workgroup barrier, so
-    // waves without tiles join it too).
+    // while tile i is computed; its V rows go to LDS buffer (i+1) % 2 at the
+    // end of the iteration.  The fused append runs before each wave's last
+    // tile (a workgroup barrier, so waves without tiles join it too).
     Tile cur, nxt;
-    if (ntiles > 0) load_tile(cur, 0);
+    if (ntiles > 0) {
+        load_tile(cur, 0);
+        stage_v(cur, s_v[wave][0]);
+    }
     for (int it = 0; it < ntiles; it++) {
         const int base = wbase + it * kMBStep;
         const bool last = it + 1 == ntiles;
         if (!last) load_tile(nxt, it + 1);
+        int8_t* vt = s_v[wave][it & 1];
         if (last && app) {
             append_part2();
-            substitute_new(cur, base);
+            substitute_new(cur, base, vt);
         }
-        int8_t* vt = s_v[wave][it & 1];
-        stage_v(cur, vt);
         compute(cur, base, vt);
-        if (!last) cur = nxt;
+        if (!last) {
+            stage_v(nxt, s_v[wave][(it + 1) & 1]);
+            cur = nxt;
+        }
     }
     if (ntiles == 0 && app) append_part2();
 
-
     // Wave results to LDS: the softmax sum over the 4 lane groups, and the
-    // accumulator rescaled from the weight max mv to the score max m.
+    // accumulator in output units (relative to the score max m).
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
-    const float fct = (m == -INFINITY || mv == -INFINITY) ? 0.0f : fast_exp2(mv - m) * (1.0f / kPScale);
+    const float fct = vref * (1.0f / kPScale);
 #pragma unroll
     for (int c = 0; c < 8; c++) {
 #pragma unroll
