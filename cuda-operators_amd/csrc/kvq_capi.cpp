@@ -42,8 +42,8 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // Split count and workspace layout for one decode problem.
 // aligned: q, caches and new rows are 16-byte aligned (vector loads);
-// quads: the matrix-core kernel may load 4 consecutive scales as one float4
-// (scale arrays 16-byte aligned, capacity a multiple of 4);
+// quads: the matrix-core kernel's layout needs hold (scale arrays 16-byte
+// aligned, capacity a multiple of 4 and below 2^24);
 // max_splits bounds the splits (scratch capacity of the reference ABI);
 // fused selects the arrival-counter merge (workspace holds counters).
 DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, bool quads, int requested,
@@ -212,13 +212,16 @@ bool decode_aligned(const kvq_decode_params* p) {
            (!p->k_new || (aligned16(p->k_new) && aligned16(p->v_new)));
 }
 
-bool decode_scale_quads(const kvq_decode_params* p) {
-    return aligned16(p->k_scale) && aligned16(p->v_scale) && (p->capacity % 4) == 0;
+// The matrix-core kernel reads 4 consecutive scales as one 16-byte load and
+// addresses a (batch, kv head) cache row through a buffer resource with 32-bit
+// byte offsets (capacity * head_dim < 2^31).
+bool decode_mfma_layout(const kvq_decode_params* p) {
+    return aligned16(p->k_scale) && aligned16(p->v_scale) && (p->capacity % 4) == 0 && p->capacity < (1 << 24);
 }
 
 DecodePlan decode_plan(const kvq_decode_params* p) {
     return make_plan(p->batch, p->num_q_heads, p->num_kv_heads, p->head_dim, decode_max_len(p),
-                     decode_aligned(p), decode_scale_quads(p), p->num_splits, INT_MAX, true);
+                     decode_aligned(p), decode_mfma_layout(p), p->num_splits, INT_MAX, true);
 }
 
 }  // namespace

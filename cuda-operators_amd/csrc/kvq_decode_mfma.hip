@@ -187,10 +187,14 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     const bool lo_row = ((r / G) & 1) != 0;
     const float qs = qdeq * a.scale_log2;  // integer dot -> score in log2 units (after x k_scale)
 
-    const int8_t* kbase = a.k + row0 * kMD;
-    const int8_t* vbase = a.v + row0 * kMD;
-    const float* ksb = a.ks + row0;
-    const float* vsb = a.vs + row0;
+    // This (batch, kv head)'s cache rows as buffer resources: tile loads add a
+    // fixed per-lane offset to a wave-uniform tile offset, and a tail tile's
+    // reads past the capacity return 0.
+    const unsigned cap = static_cast<unsigned>(a.cap);
+    const buf_rsrc kres = make_rsrc(a.k + row0 * kMD, cap * kMD);
+    const buf_rsrc vres = make_rsrc(a.v + row0 * kMD, cap * kMD);
+    const buf_rsrc ksres = make_rsrc(a.ks + row0, cap * 4u);
+    const buf_rsrc vsres = make_rsrc(a.vs + row0, cap * 4u);
 
     // The transposed V reads: lanes 2rr + h2 of group g address row R(rr),
     // half h2, of each 16-dim piece.
@@ -226,55 +230,36 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         int4 v[4];
         float ks[2][4], vs[2][4];
     };
-    const int wbase = t0 + wave * kMTile;
+    const int wbase = t0 + __builtin_amdgcn_readfirstlane(wave) * kMTile;  // wave-uniform
     const int ntiles = wbase < tend ? (tend - wbase + kMBStep - 1) / kMBStep : 0;
-    // Lane pointers for tile base `wbase`; a full tile advances them by a
-    // constant (the host guarantees 16-byte aligned scale quads), only a tile
-    // reaching past tend clamps per token.
-    const int8_t* kp0 = kbase + (static_cast<unsigned>(wbase + r) * kMD + 16 * g);
-    const int8_t* vp0 = vbase + (static_cast<unsigned>(wbase + (lane >> 3)) * kMD + 16 * (lane & 7));
-    const float* ksp0 = ksb + (wbase + 4 * g);
-    const float* vsp0 = vsb + (wbase + 4 * g);
+    // Lane byte offsets within a tile: K row r, dims 16g.. (+64 for the second
+    // 64-dim block, +16 rows for sub-tile 1); V row lane/8, 16-byte piece
+    // lane%8 (+8 rows per c); scales of tokens 4g..4g+3 (+16 tokens for s = 1).
+    const int kvo = r * kMD + 16 * g;
+    const int vvo = (lane >> 3) * kMD + 16 * (lane & 7);
+    const int svo = 16 * g;
     auto load_tile = [&](Tile& T, int it) {
         const int base = wbase + it * kMBStep;
-        if (base + kMTile <= tend) {
-            const int8_t* kp = kp0 + static_cast<size_t>(it) * (kMBStep * kMD);
-            const int8_t* vp = vp0 + static_cast<size_t>(it) * (kMBStep * kMD);
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
-                const int4 x0 = load16_stream(kp + s * 16 * kMD), x1 = load16_stream(kp + s * 16 * kMD + 64);
-                T.ka[s][0] = i32x4{x0.x, x0.y, x0.z, x0.w};
-                T.ka[s][1] = i32x4{x1.x, x1.y, x1.z, x1.w};
-            }
-#pragma unroll
-            for (int c = 0; c < 4; c++) T.v[c] = load16_stream(vp + c * 8 * kMD);
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
-                load_scales<4>(ksp0 + it * kMBStep + 16 * s, T.ks[s]);
-                load_scales<4>(vsp0 + it * kMBStep + 16 * s, T.vs[s]);
-            }
-            return;
-        }
+        const int ko = base * kMD;
+        const int so = base * 4;
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            const unsigned tc = min(base + 16 * s + r, tend - 1);
-            const int8_t* kr = kbase + (tc * kMD + 16 * g);
-            const int4 x0 = load16_stream(kr), x1 = load16_stream(kr + 64);
-            T.ka[s][0] = i32x4{x0.x, x0.y, x0.z, x0.w};
-            T.ka[s][1] = i32x4{x1.x, x1.y, x1.z, x1.w};
+            T.ka[s][0] = buffer_load16_stream(kres, kvo + s * 16 * kMD, ko);
+            T.ka[s][1] = buffer_load16_stream(kres, kvo + s * 16 * kMD + 64, ko);
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const unsigned tc = min(base + 8 * c + (lane >> 3), tend - 1);
-            T.v[c] = load16_stream(vbase + (tc * kMD + 16 * (lane & 7)));
+            const v4i_t x = buffer_load16_stream(vres, vvo + c * 8 * kMD, ko);
+            T.v[c] = make_int4(x.x, x.y, x.z, x.w);
         }
 #pragma unroll
         for (int s = 0; s < 2; s++) {
+            const v4i_t xk = buffer_load16(ksres, svo + 64 * s, so);
+            const v4i_t xv = buffer_load16(vsres, svo + 64 * s, so);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int tc = min(base + 16 * s + 4 * g + i, tend - 1);
-                T.ks[s][i] = ksb[tc];
-                T.vs[s][i] = vsb[tc];
+                T.ks[s][i] = __int_as_float(xk[i]);
+                T.vs[s][i] = __int_as_float(xv[i]);
             }
         }
     };
@@ -311,7 +296,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             *reinterpret_cast<int4*>(vt + rw * kMD + ((lane ^ (rw & 7)) << 4)) =
                 *reinterpret_cast<const int4*>(&s_newq[1][16 * lane]);
     };
-    auto compute = [&](const Tile& T, int base, const int8_t* vt) {
+    // check_tail: the tile may reach past tend (only a wave's last tile can).
+    auto compute = [&](const Tile& T, int base, const int8_t* vt, bool check_tail) {
         // QK: C[token 4g + i][row r] per sub-tile and limb.
         i32x4 cq[2][3];
 #pragma unroll
@@ -326,7 +312,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         }
         // Scores in log2 units, k-slot order s*4 + i: the low limbs combine
         // exactly in int32 ((C1 << 8) + C2 < 2^30), the top limb in fp32.
-        float sc[8];
+        float sc[8], vsv[8];
         float mt = -INFINITY, vmax = 0.0f;
 #pragma unroll
         for (int s = 0; s < 2; s++) {
@@ -335,19 +321,28 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
                 const int low = (cq[s][1][i] << 8) + cq[s][2][i];
                 const float dot = static_cast<float>(cq[s][0][i]) * 65536.0f + static_cast<float>(low);
                 sc[4 * s + i] = (dot * T.ks[s][i]) * qs;
-                vmax = fmaxf(vmax, fabsf(T.vs[s][i]));
+                vsv[4 * s + i] = T.vs[s][i];
             }
         }
-        if (base + kMTile > tend) {  // tail tile: tokens past tend do not count
+        if (check_tail && base + kMTile > tend) {
+            // Tail tile: tokens past tend (the next split's, or whatever the
+            // cache holds past the sequence) get no weight, whatever their
+            // scales hold.
 #pragma unroll
             for (int s = 0; s < 2; s++) {
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    if (base + 16 * s + 4 * g + i >= tend) sc[4 * s + i] = -INFINITY;
+                    if (base + 16 * s + 4 * g + i >= tend) {
+                        sc[4 * s + i] = -INFINITY;
+                        vsv[4 * s + i] = 0.0f;
+                    }
             }
         }
 #pragma unroll
-        for (int k = 0; k < 8; k++) mt = fmaxf(mt, sc[k]);
+        for (int k = 0; k < 8; k++) {
+            mt = fmaxf(mt, sc[k]);
+            vmax = fmaxf(vmax, fabsf(vsv[k]));
+        }
         mt = fmaxf(mt, __shfl_xor(mt, 16));
         mt = fmaxf(mt, __shfl_xor(mt, 32));
         vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
@@ -373,7 +368,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         for (int k = 0; k < 8; k++) {
             const float p = fast_exp2(sc[k] - ms);
             ps += p;
-            const float w = p * (T.vs[k >> 2][k & 3] * winv);
+            const float w = p * (vsv[k] * winv);
             const _Float16 hi = static_cast<_Float16>(w);
             const _Float16 lo = static_cast<_Float16>(w - static_cast<float>(hi));
             pb[k] = lo_row ? lo : hi;
@@ -390,27 +385,36 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
 
     // Software-pipelined tile loop: tile i+1's global loads are in flight
     // while tile i is computed; its V rows go to LDS buffer (i+1) % 2 at the
-    // end of the iteration.  The fused append runs before each wave's last
-    // tile (a workgroup barrier, so waves without tiles join it too).
-    Tile cur, nxt;
+    // end of the iteration.  Two register tiles alternate (the loop body is
+    // written out twice), so no tile is copied.  The fused append runs before
+    // each wave's last tile (a workgroup barrier, so waves without tiles join
+    // it too).
+    Tile ta, tb;
+    auto inner = [&](Tile& T, Tile& N, int it) {  // any tile but the last
+        load_tile(N, it + 1);
+        compute(T, wbase + it * kMBStep, s_v[wave][it & 1], false);
+        stage_v(N, s_v[wave][(it + 1) & 1]);
+    };
     if (ntiles > 0) {
-        load_tile(cur, 0);
-        stage_v(cur, s_v[wave][0]);
-    }
-    for (int it = 0; it < ntiles; it++) {
+        load_tile(ta, 0);
+        stage_v(ta, s_v[wave][0]);
+        int it = 0;
+        for (; it + 2 < ntiles; it += 2) {
+            inner(ta, tb, it);
+            inner(tb, ta, it + 1);
+        }
+        if (it + 1 < ntiles) {
+            inner(ta, tb, it);
+            ta = tb;
+            it++;
+        }
         const int base = wbase + it * kMBStep;
-        const bool last = it + 1 == ntiles;
-        if (!last) load_tile(nxt, it + 1);
         int8_t* vt = s_v[wave][it & 1];
-        if (last && app) {
+        if (app) {
             append_part2();
-            substitute_new(cur, base, vt);
+            substitute_new(ta, base, vt);
         }
-        compute(cur, base, vt);
-        if (!last) {
-            stage_v(nxt, s_v[wave][(it + 1) & 1]);
-            cur = nxt;
-        }
+        compute(ta, base, vt, true);
     }
     if (ntiles == 0 && app) append_part2();
 

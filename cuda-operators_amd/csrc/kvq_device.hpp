@@ -91,6 +91,28 @@ __device__ __forceinline__ int4 load16_stream(const int8_t* p) {
 #endif
 }
 
+// Raw buffer resource over [base, base + bytes) (gfx9 descriptor word 3 =
+// 0x00020000: 32-bit data format, no swizzle, stride 0).  A load through it
+// adds a per-lane byte offset (VGPR), a wave-uniform byte offset (SGPR) and an
+// immediate, so a tile loop advances one scalar instead of 64-bit lane
+// addresses; bytes at or past `bytes` read as 0.
+typedef __amdgpu_buffer_rsrc_t buf_rsrc;
+
+__device__ __forceinline__ buf_rsrc make_rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                             0x00020000);
+}
+
+// 16 bytes of streamed cache data (non-temporal, as load16_stream).
+__device__ __forceinline__ v4i_t buffer_load16_stream(buf_rsrc r, int voff, int soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, KVQ_NT_LOADS ? 2 : 0);
+}
+
+// 4 consecutive fp32 values (16 bytes).
+__device__ __forceinline__ v4i_t buffer_load16(buf_rsrc r, int voff, int soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+
 // v_exp_f32: 2^x, exp2(-inf) == 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -233,3 +233,23 @@ def test_mfma_extreme_scales(o):
     got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"])[0]
     want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"])
     assert_close(got, want, what="mfma extreme scales")
+
+
+@pytest.mark.parametrize("splits", [1, 5])
+def test_mfma_ignores_slots_past_length(o, splits):
+    """Cache slots past each sequence's length hold NaN/Inf scales and the last
+    tile of a wave reaches into them (and past the capacity): they must get no
+    weight.  Also negative v scales, which the weight normalisation takes by
+    magnitude."""
+    rng = np.random.default_rng(31 + splits)
+    B, Hkv, G, cap, d = 4, 2, 4, 1028, 128
+    lengths = np.array([1028, 1, 161, 700], np.int32)
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, lengths=lengths)
+    for b, n in enumerate(lengths):
+        p["ks"][b, :, n:] = np.float32(np.nan)
+        p["vs"][b, :, n:] = np.float32(np.inf)
+    p["vs"][2, 1, :100] *= np.float32(-1.0)
+    got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths, splits=splits)[0]
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert np.isfinite(got).all()
+    assert_close(got, want, what=f"mfma slots past length, splits {splits}")
