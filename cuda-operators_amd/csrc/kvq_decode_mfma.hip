@@ -85,8 +85,14 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     static_assert(G == 4 || G == 8, "heads per workgroup");
     constexpr int NT = kMWaves * kWave;
     static_assert(NT == 2 * kMD, "the fused append gives one K or V element to each thread");
-    __shared__ __align__(16) int8_t s_v[kMWaves][2][kMTile * kMD];
-    __shared__ __align__(16) float s_acc[kMWaves][16][kMD];
+    // V tile buffers during the tile loop; the waves' results afterwards.
+    union TileOrResult {
+        int8_t v[kMWaves][2][kMTile * kMD];
+        float acc[kMWaves][16][kMD];
+    };
+    __shared__ __align__(16) TileOrResult s_u;
+    auto& s_v = s_u.v;
+    auto& s_acc = s_u.acc;
     __shared__ float s_ml[kMWaves][G][2];
     __shared__ __align__(16) int8_t s_newq[2][kMD];
     __shared__ float s_newscale[2];
@@ -422,6 +428,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // accumulator in output units (relative to the score max m).
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
+    __syncthreads();  // every wave is done with its V tiles (s_acc reuses them)
     const float fct = vref * (1.0f / kPScale);
 #pragma unroll
     for (int c = 0; c < 8; c++) {

@@ -113,6 +113,11 @@ __device__ __forceinline__ v4i_t buffer_load16(buf_rsrc r, int voff, int soff) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
 }
 
+// One 32-bit word.
+__device__ __forceinline__ int buffer_load4(buf_rsrc r, int voff, int soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+
 // v_exp_f32: 2^x, exp2(-inf) == 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -81,70 +81,122 @@ __device__ __forceinline__ void store_result(const DecodeArgs& a, size_t bhq, in
     }
 }
 
-// Merge of one sequence group's records by a whole workgroup (nthreads
-// threads, nheads <= kMergeHeads, nsplit <= kMergeSplits): per head the max
-// and the weights exp2(m_s - M) are computed once, in parallel over splits,
-// then every output element sums its nsplit accumulators with 8 loads in
-// flight.
+// Merge of one sequence group's records by a whole workgroup (nheads <=
+// kMergeHeads, nsplit <= kMergeSplits, d % 4 == 0, the group's records below
+// 2 GiB).  Every load is issued with as many others in flight as registers
+// allow, since the merge runs after the rest of the launch has drained and
+// its latency adds directly to the step time:
+// 1. one coherent 8-byte load per (head, split) for (m, l), into LDS;
+// 2. per head (one wave each): M = max m, the weights exp2(m - M) and
+//    L = sum l * weight;
+// 3. the accumulators as coherent 16-byte loads, 16 in flight per thread,
+//    threads splitting the splits of a column when there are fewer columns
+//    than threads; out = (sum acc * weight) / L.
 constexpr int kMergeHeads = 8;
 constexpr int kMergeSplits = 256;
+constexpr int kMergeMaxThreads = 512;
+constexpr int kCoherent = 16;  // buffer-load cache policy: sc1, device-coherent (as get_coherent)
+
+__device__ inline bool merge_group_fits(const DecodeArgs& a, int nheads, int nsplit) {
+    return nheads <= kMergeHeads && nsplit <= kMergeSplits && (a.d & 3) == 0 &&
+           static_cast<long>(nheads) * a.splits * a.d < (1L << 29) && blockDim.x <= kMergeMaxThreads;
+}
 
 __device__ inline void merge_group(const DecodeArgs& a, size_t bhq0, int nheads, int nsplit) {
-    __shared__ float s_w[kMergeHeads][kMergeSplits];
-    __shared__ float s_red[kMergeHeads][16];
-    __shared__ float s_inv[kMergeHeads];
-    const int nthreads = blockDim.x;
-    const int nw = nthreads / kWave;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    for (int h = 0; h < nheads; h++) {
-        const float* ml = a.part_ml + (bhq0 + h) * a.splits * 2;
-        float mx = -INFINITY;
-        for (int sp = threadIdx.x; sp < nsplit; sp += nthreads) {
-            const float mv = get_coherent(ml + 2 * sp);
-            s_w[h][sp] = mv;
-            mx = fmaxf(mx, mv);
+    __shared__ float s_w[kMergeHeads][kMergeSplits];  // m, then the weights
+    __shared__ float s_L[kMergeHeads];
+    union LOrPart {
+        float l[kMergeHeads][kMergeSplits];  // phases 1-2
+        float4 part[kMergeMaxThreads];       // phase 3
+    };
+    __shared__ LOrPart s_x;
+    const int T = blockDim.x;
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = t / kWave;
+    const int nw = T / kWave;
+    const int S = a.splits;
+    const int d = a.d;
+    const buf_rsrc mlr = make_rsrc(a.part_ml + bhq0 * S * 2, static_cast<unsigned>(nheads * S * 8));
+    const buf_rsrc accr = make_rsrc(a.part_acc + bhq0 * S * d, static_cast<unsigned>(nheads * S * d * 4));
+
+    const int npairs = nheads * nsplit;  // <= 2048, so at most 8 per thread
+#pragma unroll
+    for (int k = 0; k < kMergeHeads * kMergeSplits / 256; k++) {
+        const int i = t + k * T;
+        if (i < npairs) {
+            const int h = i / nsplit;
+            const int sp = i - h * nsplit;
+            typedef int v2i_t __attribute__((ext_vector_type(2)));
+            const v2i_t x = __builtin_amdgcn_raw_buffer_load_b64(mlr, (h * S + sp) * 8, 0, kCoherent);
+            s_w[h][sp] = __int_as_float(x.x);
+            s_x.l[h][sp] = __int_as_float(x.y);
         }
-        mx = wave_max(mx);
-        if (lane == 0) s_red[h][wave] = mx;
     }
     __syncthreads();
-    for (int h = 0; h < nheads; h++) {
-        const float* ml = a.part_ml + (bhq0 + h) * a.splits * 2;
-        float M = -INFINITY;
-        for (int w = 0; w < nw; w++) M = fmaxf(M, s_red[h][w]);
-        float lsum = 0.0f;
-        for (int sp = threadIdx.x; sp < nsplit; sp += nthreads) {
+    for (int h = wave; h < nheads; h += nw) {
+        float mx = -INFINITY;
+        for (int sp = lane; sp < nsplit; sp += kWave) mx = fmaxf(mx, s_w[h][sp]);
+        mx = wave_max(mx);
+        const float M = mx == -INFINITY ? 0.0f : mx;
+        float L = 0.0f;
+        for (int sp = lane; sp < nsplit; sp += kWave) {
             const float w = fast_exp2(s_w[h][sp] - M);
             s_w[h][sp] = w;
-            lsum = fmaf(get_coherent(ml + 2 * sp + 1), w, lsum);
+            L = fmaf(s_x.l[h][sp], w, L);
         }
-        lsum = wave_sum(lsum);
-        __syncthreads();  // every wave has read s_red[h] before it is reused
-        if (lane == 0) s_red[h][wave] = lsum;
+        L = wave_sum(L);
+        if (lane == 0) s_L[h] = L;
     }
     __syncthreads();
-    if (threadIdx.x < nheads) {
-        float L = 0.0f;
-        for (int w = 0; w < nw; w++) L += s_red[threadIdx.x][w];
-        s_inv[threadIdx.x] = L;
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < nheads * a.d; i += nthreads) {
-        const int h = i / a.d;
-        const int dim = i - h * a.d;
-        const float* acc = a.part_acc + (bhq0 + h) * a.splits * a.d + dim;
-        float A = 0.0f;
-        int sp = 0;
-        for (; sp + 8 <= nsplit; sp += 8) {
-            float v[8];
+    const int cpr = d >> 2;  // 16-byte columns per head
+    const int ncols = nheads * cpr;
+    const int groups = max(1, min(T / ncols, nsplit));
+    for (int item = t; item < ncols * groups; item += T) {
+        const int j = item / ncols;
+        const int c = item - j * ncols;
+        const int h = c / cpr;
+        const int off0 = (h * S * d + 4 * (c - h * cpr)) * 4;
+        float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int sp0 = j; sp0 < nsplit; sp0 += 16 * groups) {
+            v4i_t v[16];
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = get_coherent(acc + static_cast<size_t>(sp + j) * a.d);
+            for (int k = 0; k < 16; k++) {
+                const int sp = sp0 + k * groups;
+                v[k] = sp < nsplit ? __builtin_amdgcn_raw_buffer_load_b128(accr, off0 + sp * d * 4, 0, kCoherent)
+                                   : v4i_t{0, 0, 0, 0};
+            }
 #pragma unroll
-            for (int j = 0; j < 8; j++) A = fmaf(v[j], s_w[h][sp + j], A);
+            for (int k = 0; k < 16; k++) {
+                const int sp = sp0 + k * groups;
+                const float w = sp < nsplit ? s_w[h][sp] : 0.0f;
+                A.x = fmaf(__int_as_float(v[k].x), w, A.x);
+                A.y = fmaf(__int_as_float(v[k].y), w, A.y);
+                A.z = fmaf(__int_as_float(v[k].z), w, A.z);
+                A.w = fmaf(__int_as_float(v[k].w), w, A.w);
+            }
         }
-        for (; sp < nsplit; sp++) A = fmaf(get_coherent(acc + static_cast<size_t>(sp) * a.d), s_w[h][sp], A);
-        a.out[(bhq0 + h) * a.d + dim] = A / s_inv[h];
+        if (groups > 1) {
+            s_x.part[item] = A;
+        } else {
+            float* o = a.out + (bhq0 + h) * d + 4 * (c - h * cpr);
+            const float L = s_L[h];
+            o[0] = A.x / L, o[1] = A.y / L, o[2] = A.z / L, o[3] = A.w / L;
+        }
+    }
+    if (groups > 1) {
+        __syncthreads();
+        for (int c = t; c < ncols; c += T) {
+            float4 A = s_x.part[c];
+            for (int j = 1; j < groups; j++) {
+                const float4 x = s_x.part[j * ncols + c];
+                A.x += x.x, A.y += x.y, A.z += x.z, A.w += x.w;
+            }
+            const int h = c / cpr;
+            float* o = a.out + (bhq0 + h) * d + 4 * (c - h * cpr);
+            const float L = s_L[h];
+            o[0] = A.x / L, o[1] = A.y / L, o[2] = A.z / L, o[3] = A.w / L;
+        }
     }
 }
 
@@ -162,7 +214,7 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, int unit, size
     }
     __syncthreads();
     if (*s_last) {
-        if (nheads <= kMergeHeads && nsplit <= kMergeSplits) {
+        if (merge_group_fits(a, nheads, nsplit)) {
             merge_group(a, bhq0, nheads, nsplit);
         } else {
             for (int i = threadIdx.x; i < nheads * a.d; i += blockDim.x) {
