@@ -28,13 +28,19 @@ constexpr size_t kAlign = 256;
 // than counters use the separate merge kernel instead.
 constexpr size_t kCounterBytes = 256 * 1024;
 constexpr long kMaxCounters = static_cast<long>(kCounterBytes / sizeof(int));
-// Workgroups a decode launch aims for when it picks the split count itself:
-// 8 per CU on MI355X's 256 CUs.
 // Workgroups a decode launch aims for when it picks the split count itself
 // (MI355X: 256 CUs).  An 8-wave VALU workgroup fills a CU's issue slots on its
 // own; two 4-wave MFMA workgroups share a CU.
 constexpr int kTargetWorkgroupsValu = 256;
 constexpr int kTargetWorkgroupsMfma = 512;
+// The same for the device split schedule of a ragged batch (work items of
+// equal size, so the target is the number of chunks over the whole batch).
+#ifndef KVQ_SCHED_TARGET_VALU
+#define KVQ_SCHED_TARGET_VALU 512
+#endif
+#ifndef KVQ_SCHED_TARGET_MFMA
+#define KVQ_SCHED_TARGET_MFMA 512
+#endif
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -44,10 +50,11 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // aligned: q, caches and new rows are 16-byte aligned (vector loads);
 // quads: the matrix-core kernel's layout needs hold (scale arrays 16-byte
 // aligned, capacity a multiple of 4 and below 2^24);
+// ragged: per-sequence lengths on the device;
 // max_splits bounds the splits (scratch capacity of the reference ABI);
 // fused selects the arrival-counter merge (workspace holds counters).
-DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, bool quads, int requested,
-                     int max_splits, bool fused) {
+DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, bool quads, bool ragged,
+                     int requested, int max_splits, bool fused) {
     DecodePlan p{};
     const int G = Hq / Hkv;
     const int sg_m = kvq::mfma_heads_per_group(G, d);
@@ -70,6 +77,24 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
     const long units = p.fast ? static_cast<long>(B) * Hkv * p.nsg : static_cast<long>(B) * Hq;
     const int gran = p.fast ? tile : 64;
     max_len = std::max(max_len, 1);
+    if (ragged && requested == 0 && fused && p.fast && units <= kMaxCounters) {
+        // Ragged batch: the split schedule is computed on the device from the
+        // lengths.  Items (and records) <= B + target / units per sequence.
+        const int U = Hkv * p.nsg;
+        p.scheduled = true;
+        p.counters = true;
+        p.sched_target = p.kernel == kvq::Kernel::Mfma ? KVQ_SCHED_TARGET_MFMA : KVQ_SCHED_TARGET_VALU;
+        p.sched_gran = gran;
+        p.sched_items = B + (p.sched_target + U - 1) / U + 1;
+        p.splits = 0;
+        p.chunk = 0;
+        const size_t recs = static_cast<size_t>(p.sched_items) * Hq;
+        p.counter_bytes = kCounterBytes;
+        p.sched_bytes = round_up((kvq::kSchedHeader + 2 * static_cast<size_t>(p.sched_items) + B) * sizeof(int), kAlign);
+        p.ml_bytes = round_up(recs * 2 * sizeof(float), kAlign);
+        p.acc_bytes = round_up(recs * static_cast<size_t>(d) * sizeof(float), kAlign);
+        return p;
+    }
     long splits;
     int chunk;
     if (requested > 0) {
@@ -101,13 +126,17 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
     return p;
 }
 
-size_t plan_bytes(const DecodePlan& p) { return p.counter_bytes + p.ml_bytes + p.acc_bytes; }
+size_t plan_bytes(const DecodePlan& p) { return p.counter_bytes + p.sched_bytes + p.ml_bytes + p.acc_bytes; }
 
+// Workspace: [counters][split schedule][partial (m, l)][partial accumulators].
 void bind_workspace(DecodeArgs& a, const DecodePlan& p, void* ws) {
     char* base = static_cast<char*>(ws);
     a.counters = p.counters ? reinterpret_cast<int*>(base) : nullptr;
-    a.part_ml = p.splits > 1 ? reinterpret_cast<float*>(base + p.counter_bytes) : nullptr;
-    a.part_acc = p.splits > 1 ? reinterpret_cast<float*>(base + p.counter_bytes + p.ml_bytes) : nullptr;
+    a.sched = p.scheduled ? reinterpret_cast<const int*>(base + p.counter_bytes) : nullptr;
+    a.sched_items = p.sched_items;
+    const size_t ml = p.counter_bytes + p.sched_bytes;
+    a.part_ml = p.ml_bytes ? reinterpret_cast<float*>(base + ml) : nullptr;
+    a.part_acc = p.acc_bytes ? reinterpret_cast<float*>(base + ml + p.ml_bytes) : nullptr;
 }
 
 bool shape_ok(int H, int N, int d) { return H > 0 && N > 0 && d > 0 && d <= KVQ_MAX_HEAD_DIM; }
@@ -145,7 +174,7 @@ hipError_t reference_launch(const float* Q, const int8_t* K, const int8_t* V, co
     DecodeArgs a = reference_args(Q, K, V, ks, vs, out, H, N, d);
     // S holds H*N floats; a split needs (d + 2) floats per head.
     const int max_splits = std::max(1, N / (d + 2));
-    const DecodePlan p = make_plan(1, H, H, d, N, reference_aligned(Q, K, V, d), false, 0, max_splits, false);
+    const DecodePlan p = make_plan(1, H, H, d, N, reference_aligned(Q, K, V, d), false, false, 0, max_splits, false);
     a.splits = p.splits;
     a.chunk = p.chunk;
     a.nsg = p.nsg;
@@ -221,7 +250,7 @@ bool decode_mfma_layout(const kvq_decode_params* p) {
 
 DecodePlan decode_plan(const kvq_decode_params* p) {
     return make_plan(p->batch, p->num_q_heads, p->num_kv_heads, p->head_dim, decode_max_len(p),
-                     decode_aligned(p), decode_mfma_layout(p), p->num_splits, INT_MAX, true);
+                     decode_aligned(p), decode_mfma_layout(p), p->lengths != nullptr, p->num_splits, INT_MAX, true);
 }
 
 }  // namespace
@@ -243,7 +272,7 @@ void solve(const float* Q, const int8_t* K_int8, const int8_t* V_int8, const flo
     }
     DecodeArgs a = reference_args(Q, K_int8, V_int8, k_scale, v_scale, output, num_heads, seq_len, head_dim);
     const DecodePlan p = make_plan(1, num_heads, num_heads, head_dim, seq_len,
-                                   reference_aligned(Q, K_int8, V_int8, head_dim), false, 0, INT_MAX, true);
+                                   reference_aligned(Q, K_int8, V_int8, head_dim), false, false, 0, INT_MAX, true);
     a.splits = p.splits;
     a.chunk = p.chunk;
     a.nsg = p.nsg;

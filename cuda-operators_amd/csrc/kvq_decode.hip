@@ -130,27 +130,26 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     const int tg = lane / LPT;  // token slot within a wave load
     const int ds = lane % LPT;  // 16-element slice of the head dim
 
-    const int units = a.B * a.Hkv * a.nsg;
-    const int split = blockIdx.x / units;
-    const int unit = blockIdx.x - split * units;
+    SplitWork w;
+    if (!locate_work(a, w)) return;
+    const int unit = w.unit;
     const int bh = unit / a.nsg;
     const int sgi = unit - bh * a.nsg;
     const int b = bh / a.Hkv;
     const int kvh = bh - b * a.Hkv;
     const int hq0 = kvh * a.G + sgi * SG;
     const size_t bhq0 = static_cast<size_t>(b) * a.Hq + hq0;
-    const int len = seq_len_of(a, b);
-    const int nsplit = (len + a.chunk - 1) / a.chunk;
+    const int len = w.len;
+    const int split = w.split;
+    const int nsplit = w.nsplit;
 
     if (len == 0) {
-        if (split == 0)
-            for (int i = threadIdx.x; i < SG * D; i += blockDim.x) a.out[bhq0 * D + i] = 0.0f;
+        for (int i = threadIdx.x; i < SG * D; i += blockDim.x) a.out[bhq0 * D + i] = 0.0f;
         return;
     }
-    if (split >= nsplit) return;
 
-    const int t0 = split * a.chunk;
-    const int t1 = min(len, t0 + a.chunk);
+    const int t0 = w.t0;
+    const int t1 = w.t1;
     const bool app = (a.k_new != nullptr) && (t1 == len);
     const int tend = app ? t1 - 1 : t1;  // tokens read from the cache
 
@@ -346,6 +345,7 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     __syncthreads();
 
     // Merge the waves; one thread per (head, element).
+    const RecMap map = nsplit > 1 ? rec_map(a, b, bhq0) : RecMap{0, 0, 0};
     for (int i = threadIdx.x; i < SG * D; i += blockDim.x) {
         const int h = i / D;
         const int dim = i - h * D;
@@ -360,9 +360,9 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
             L = fmaf(s_ml[w][h][1], f, L);
             A = fmaf(s_acc[w][h][dim], f, A);
         }
-        store_result(a, bhq0 + h, dim, split, nsplit, M, L, A);
+        store_result(a, map, bhq0, h, dim, split, nsplit, M, L, A);
     }
-    finish_split(a, unit, bhq0, SG, nsplit, &s_last);
+    finish_split(a, unit, map, bhq0, SG, nsplit, &s_last);
 }
 
 __global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a) {
@@ -371,8 +371,9 @@ __global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a) {
     const int len = seq_len_of(a, b);
     const int nsplit = (len + a.chunk - 1) / a.chunk;
     if (nsplit <= 1) return;  // written directly by the decode kernel
+    const RecMap map = rec_map(a, b, bhq);
     for (int dim = threadIdx.x; dim < a.d; dim += blockDim.x)
-        a.out[static_cast<size_t>(bhq) * a.d + dim] = merge_dim(a, bhq, dim, nsplit);
+        a.out[static_cast<size_t>(bhq) * a.d + dim] = merge_dim(a, map, 0, dim, nsplit);
 }
 
 __global__ __launch_bounds__(kWave) void decode_generic(const DecodeArgs a) {
@@ -436,7 +437,7 @@ __global__ __launch_bounds__(kWave) void decode_generic(const DecodeArgs a) {
 
 template <int D>
 hipError_t launch_fast_d(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(a.B * a.Hkv * p.nsg * p.splits));
+    const dim3 grid(static_cast<unsigned>(decode_grid(a, p)));
     const dim3 block(kFastWaves * kWave);
     switch (p.sg) {
         case 1: hipLaunchKernelGGL((decode_fast<D, 1>), grid, block, 0, stream, a); break;
@@ -480,8 +481,18 @@ hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+long decode_grid(const DecodeArgs& a, const DecodePlan& p) {
+    const long units = static_cast<long>(a.Hkv) * p.nsg;
+    return p.scheduled ? units * p.sched_items : units * a.B * p.splits;
+}
+
 hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
     hipError_t err;
+    if (p.scheduled) {
+        err = launch_schedule(a.lengths, a.B, a.max_len, a.Hkv * p.nsg, p.sched_target, p.sched_gran,
+                              p.sched_items, const_cast<int*>(a.sched), stream);
+        if (err != hipSuccess) return err;
+    }
     if (p.kernel == Kernel::Mfma) {
         err = launch_decode_mfma(a, p, stream);
         if (err != hipSuccess) return err;

@@ -104,27 +104,26 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     const int r = lane & 15;   // MFMA row / token-in-subtile index
     const int g = lane >> 4;   // 16-lane group
 
-    const int units = a.B * a.Hkv * a.nsg;
-    const int split = blockIdx.x / units;
-    const int unit = blockIdx.x - split * units;
+    SplitWork w;
+    if (!locate_work(a, w)) return;
+    const int unit = w.unit;
     const int bh = unit / a.nsg;
     const int sgi = unit - bh * a.nsg;
     const int b = bh / a.Hkv;
     const int kvh = bh - b * a.Hkv;
     const int hq0 = kvh * a.G + sgi * G;
     const size_t bhq0 = static_cast<size_t>(b) * a.Hq + hq0;
-    const int len = seq_len_of(a, b);
-    const int nsplit = (len + a.chunk - 1) / a.chunk;
+    const int len = w.len;
+    const int split = w.split;
+    const int nsplit = w.nsplit;
 
     if (len == 0) {
-        if (split == 0)
-            for (int i = threadIdx.x; i < G * kMD; i += blockDim.x) a.out[bhq0 * kMD + i] = 0.0f;
+        for (int i = threadIdx.x; i < G * kMD; i += blockDim.x) a.out[bhq0 * kMD + i] = 0.0f;
         return;
     }
-    if (split >= nsplit) return;
 
-    const int t0 = split * a.chunk;
-    const int tend = min(len, t0 + a.chunk);
+    const int t0 = w.t0;
+    const int tend = w.t1;
     const bool app = (a.k_new != nullptr) && (tend == len);
     const int tnew = len - 1;
     const size_t row0 = static_cast<size_t>(bh) * a.cap;
@@ -442,6 +441,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     __syncthreads();
 
     // Merge the waves and the hi/lo rows; one thread per (head, element).
+    const RecMap map = nsplit > 1 ? rec_map(a, b, bhq0) : RecMap{0, 0, 0};
     for (int i = threadIdx.x; i < G * kMD; i += blockDim.x) {
         const int h = i / kMD;
         const int dim = i - h * kMD;
@@ -456,9 +456,9 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             L = fmaf(s_ml[w][h][1], f, L);
             A = fmaf(s_acc[w][h][dim] + s_acc[w][h + G][dim], f, A);
         }
-        store_result(a, bhq0 + h, dim, split, nsplit, M, L, A);
+        store_result(a, map, bhq0, h, dim, split, nsplit, M, L, A);
     }
-    finish_split(a, unit, bhq0, G, nsplit, &s_last);
+    finish_split(a, unit, map, bhq0, G, nsplit, &s_last);
 }
 
 }  // namespace
@@ -473,7 +473,7 @@ int mfma_heads_per_group(int G, int d) {
 }
 
 hipError_t launch_decode_mfma(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(a.B * a.Hkv * p.nsg * p.splits));
+    const dim3 grid(static_cast<unsigned>(decode_grid(a, p)));
     const dim3 block(kMWaves * kWave);
     switch (p.sg) {
         case 4: hipLaunchKernelGGL(decode_mfma<4>, grid, block, 0, stream, a); break;

@@ -18,17 +18,33 @@ struct DecodeArgs {
     const int32_t* lengths;  // [B] or null
     const float* k_new;      // fused append source [B, Hkv, d] or null
     const float* v_new;
-    float* part_ml;          // [B, Hq, splits, 2]  (max in log2 units, sum)
-    float* part_acc;         // [B, Hq, splits, d]  unnormalised accumulators
+    float* part_ml;          // partial records (max in log2 units, sum): [B, Hq, splits, 2],
+                             // or [records, Hq, 2] under a split schedule
+    float* part_acc;         // unnormalised accumulators, same order, d floats per record
     int* counters;           // [B * Hkv * nsg] arrival counters, or null (merge kernel)
+    const int* sched;        // split schedule written by schedule_kernel, or null (static splits)
+    int sched_items;         // capacity of the schedule's item list
     int B, Hq, Hkv, G, cap, d;
     int uniform_len;         // used when lengths == null
     int max_len;             // every length is clamped to [0, max_len], max_len <= cap
-    int splits;              // grid splits per sequence
-    int chunk;               // tokens per split
+    int splits;              // grid splits per sequence (static splits)
+    int chunk;               // tokens per split (static splits)
     int nsg;                 // head groups per kv head (G / heads per workgroup)
     float scale_log2;        // softmax_scale * log2(e)
 };
+
+// Split schedule of a ragged batch, computed on the device from the lengths
+// by schedule_kernel before the decode launch (int words):
+//   [0] chunk: tokens per split;  [1] item count;  [2], [3] unused
+//   items  [kSchedHeader, + 2 * sched_items): (batch index, split index) per
+//          work item, every split of every sequence once: whole chunks first,
+//          then each sequence's last chunk, longest first (a length-0
+//          sequence has one empty item that writes its zero output);
+//   rec_base [B] after the items: the first partial record of sequence b; its
+//          split s owns records (rec_base[b] + s) * Hq + hq.
+// Workgroup i of the decode grid takes item i / U, work unit i % U of that
+// sequence (U = Hkv * nsg).
+constexpr int kSchedHeader = 4;
 
 // Which decode kernel a plan runs.
 enum class Kernel {
@@ -46,13 +62,22 @@ struct DecodePlan {
     int splits;      // splits per sequence (grid dimension)
     int chunk;       // tokens per split
     bool counters;   // last-arriving split merges (fast path with a zeroed counter prefix)
-    size_t counter_bytes, ml_bytes, acc_bytes;  // workspace regions (0 when splits == 1)
+    bool scheduled;  // ragged batch: the split schedule is computed on the device
+    int sched_items;     // schedule item capacity (scheduled)
+    int sched_target;    // workgroups the schedule aims for (scheduled)
+    int sched_gran;      // chunk granularity in tokens (scheduled)
+    size_t counter_bytes, sched_bytes, ml_bytes, acc_bytes;  // workspace regions
 };
 
 // Kernel launchers (kvq_decode.hip / kvq_append.hip).  They do no argument
 // validation; the C ABI layer (kvq_capi.cpp) validates before calling them.
 hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& plan, hipStream_t stream);
+// Workgroups of a tuned decode kernel's grid.
+long decode_grid(const DecodeArgs& a, const DecodePlan& plan);
 hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream);
+// Writes the split schedule of a ragged batch (see kSchedHeader) to sched.
+hipError_t launch_schedule(const int32_t* lengths, int B, int max_len, int units_per_seq, int target_wgs,
+                           int gran, int items_cap, int* sched, hipStream_t stream);
 // Append one token per (b, kv head).  Position: positions[b] (or uniform_pos
 // when positions is null); with from_lengths, positions holds sequence lengths
 // and the token goes to clamp(lengths[b], 0, max_len) - 1.

@@ -1,0 +1,157 @@
+// kvq_schedule.hip -- device-side split schedule of a ragged decode batch.
+//
+// With per-sequence lengths on the device, a static split grid (every
+// sequence cut into the same number of chunks of the longest sequence's
+// length) leaves most workgroups of short sequences idle and the longest ones
+// finishing last.  One small workgroup instead reads the lengths and writes a
+// schedule (layout at kSchedHeader in kvq_internal.hpp) that the decode launch
+// right after it on the same stream follows:
+//
+// * chunk = total tokens x units per sequence / target workgroups, rounded up
+//   to the tile granularity and clamped to [gran, max_len rounded up]: about
+//   `target` equal chunks over the whole batch, whatever the length mix;
+// * whole chunks are dispatched first and each sequence's last (partial)
+//   chunk after them, longest first (64 size classes, a counting sort), so
+//   the work left at the end of the launch is small -- list scheduling in
+//   longest-processing-time order;
+// * partial records are numbered per sequence (rec_base) so the workspace
+//   holds records only for splits that exist: at most B + target / units.
+#include "kvq_device.hpp"
+#include "kvq_internal.hpp"
+
+namespace kvq {
+namespace {
+
+constexpr int kSchedThreads = 1024;
+constexpr int kSchedWaves = kSchedThreads / kWave;
+constexpr int kSizeClasses = 64;
+
+// Exclusive prefix sum of x over the workgroup (thread order); *total gets
+// the sum.  s_tmp: kSchedWaves ints of LDS, reusable after the call.
+__device__ int block_exclusive_scan(int x, int* s_tmp, int* total) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    int v = x;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int y = __shfl_up(v, off);
+        if (lane >= off) v += y;
+    }
+    if (lane == kWave - 1) s_tmp[wave] = v;
+    __syncthreads();
+    if (wave == 0) {
+        int u = lane < kSchedWaves ? s_tmp[lane] : 0;
+#pragma unroll
+        for (int off = 1; off < kSchedWaves; off <<= 1) {
+            const int y = __shfl_up(u, off);
+            if (lane >= off) u += y;
+        }
+        if (lane < kSchedWaves) s_tmp[lane] = u;
+    }
+    __syncthreads();
+    const int before = wave > 0 ? s_tmp[wave - 1] : 0;
+    *total = s_tmp[kSchedWaves - 1];
+    __syncthreads();
+    return before + v - x;
+}
+
+__device__ __forceinline__ int clamped_len(const int32_t* lengths, int b, int max_len) {
+    return min(max(lengths[b], 0), max_len);
+}
+
+__global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* lengths, int B, int max_len,
+                                                                 int units, int target, int gran, int items_cap,
+                                                                 int* sched) {
+    __shared__ int s_tmp[kSchedWaves];
+    __shared__ long long s_sum[kSchedWaves];
+    __shared__ int s_class[kSizeClasses];
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = t / kWave;
+
+    long long sum = 0;
+    for (int b = t; b < B; b += kSchedThreads) sum += clamped_len(lengths, b, max_len);
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    if (lane == 0) s_sum[wave] = sum;
+    if (t < kSizeClasses) s_class[t] = 0;
+    __syncthreads();
+    long long total = 0;
+#pragma unroll
+    for (int w = 0; w < kSchedWaves; w++) total += s_sum[w];
+
+    const long long want = (total * units + target - 1) / target;
+    const long long cmax = (static_cast<long long>(max(max_len, 1)) + gran - 1) / gran * gran;
+    const long long c = (want + gran - 1) / gran * gran;
+    const int chunk = static_cast<int>(min(cmax, max(static_cast<long long>(gran), c)));
+
+    int* items = sched + kSchedHeader;
+    int* rec_base = items + 2 * items_cap;
+    int rec_carry = 0, full_carry = 0;
+    for (int b0 = 0; b0 < B; b0 += kSchedThreads) {
+        const int b = b0 + t;
+        int len = 0, n = 0;
+        if (b < B) {
+            len = clamped_len(lengths, b, max_len);
+            n = len == 0 ? 1 : (len + chunk - 1) / chunk;
+        }
+        const int full = n > 0 ? n - 1 : 0;
+        int tot_n = 0, tot_f = 0;
+        const int pre_n = block_exclusive_scan(n, s_tmp, &tot_n);
+        const int pre_f = block_exclusive_scan(full, s_tmp, &tot_f);
+        if (b < B) {
+            rec_base[b] = rec_carry + pre_n;
+            for (int s = 0; s < full; s++) {
+                const int pos = full_carry + pre_f + s;
+                if (pos < items_cap) {
+                    items[2 * pos] = b;
+                    items[2 * pos + 1] = s;
+                }
+            }
+            const int last = len - (n - 1) * chunk;  // in [0, chunk]
+            const int cls = static_cast<int>(static_cast<long long>(chunk - last) * kSizeClasses / (chunk + 1));
+            atomicAdd(&s_class[cls], 1);
+        }
+        rec_carry += tot_n;
+        full_carry += tot_f;
+    }
+    __syncthreads();
+    // Size classes -> first item position of each class (longest first).
+    if (wave == 0) {
+        const int cnt = s_class[lane];
+        int v = cnt;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int y = __shfl_up(v, off);
+            if (lane >= off) v += y;
+        }
+        s_class[lane] = full_carry + v - cnt;
+    }
+    __syncthreads();
+    for (int b = t; b < B; b += kSchedThreads) {
+        const int len = clamped_len(lengths, b, max_len);
+        const int n = len == 0 ? 1 : (len + chunk - 1) / chunk;
+        const int last = len - (n - 1) * chunk;
+        const int cls = static_cast<int>(static_cast<long long>(chunk - last) * kSizeClasses / (chunk + 1));
+        const int pos = atomicAdd(&s_class[cls], 1);
+        if (pos < items_cap) {
+            items[2 * pos] = b;
+            items[2 * pos + 1] = n - 1;
+        }
+    }
+    if (t == 0) {
+        sched[0] = chunk;
+        sched[1] = min(full_carry + B, items_cap);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_schedule(const int32_t* lengths, int B, int max_len, int units_per_seq, int target_wgs,
+                           int gran, int items_cap, int* sched, hipStream_t stream) {
+    hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(kSchedThreads), 0, stream, lengths, B, max_len,
+                       units_per_seq, target_wgs, gran, items_cap, sched);
+    return hipGetLastError();
+}
+
+}  // namespace kvq

@@ -15,6 +15,57 @@ __device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
     return min(max(len, 0), a.max_len);
 }
 
+// What one decode workgroup computes: work unit `unit` (index (b * Hkv + kvh)
+// * nsg + sgi of (sequence, kv head, head group)) over tokens [t0, t1), split
+// `split` of the sequence's nsplit.  A length-0 sequence has one split with
+// t0 = t1 = 0 (its workgroup writes the zero output).
+struct SplitWork {
+    int unit, b, split, nsplit, len, t0, t1;
+};
+
+// Work of workgroup blockIdx.x, from the static split grid (split-major:
+// blockIdx = split * units + unit) or the device split schedule; false: the
+// workgroup has nothing to do.
+__device__ __forceinline__ bool locate_work(const DecodeArgs& a, SplitWork& w) {
+    const int U = a.Hkv * a.nsg;
+    int chunk;
+    if (a.sched) {
+        const int item = blockIdx.x / U;
+        if (item >= a.sched[1]) return false;
+        chunk = a.sched[0];
+        w.b = a.sched[kSchedHeader + 2 * item];
+        w.split = a.sched[kSchedHeader + 2 * item + 1];
+        w.unit = w.b * U + (blockIdx.x - item * U);
+    } else {
+        const int units = a.B * U;
+        w.split = blockIdx.x / units;
+        w.unit = blockIdx.x - w.split * units;
+        w.b = w.unit / U;
+        chunk = a.chunk;
+    }
+    w.len = seq_len_of(a, w.b);
+    w.nsplit = w.len == 0 ? 1 : (w.len + chunk - 1) / chunk;
+    if (w.split >= w.nsplit) return false;
+    w.t0 = w.split * chunk;
+    w.t1 = min(w.len, w.t0 + chunk);
+    return true;
+}
+
+// Partial record of row bhq0 + h, split s: r0 + h * hs + s * ss (records of
+// 2 floats in part_ml, d floats in part_acc).
+struct RecMap {
+    size_t r0;
+    int hs, ss;
+};
+
+__device__ __forceinline__ RecMap rec_map(const DecodeArgs& a, int b, size_t bhq0) {
+    if (a.sched) {
+        const int base = a.sched[kSchedHeader + 2 * a.sched_items + b];
+        return {static_cast<size_t>(base) * a.Hq + (bhq0 - static_cast<size_t>(b) * a.Hq), 1, a.Hq};
+    }
+    return {bhq0 * a.splits, a.splits, 1};
+}
+
 // U consecutive per-token scales (U in {1,2,4,8}); p is U*4-byte aligned when
 // the token index is a multiple of U (tiles start at multiples of U tokens).
 template <int U>
@@ -50,29 +101,29 @@ __device__ __forceinline__ float get_coherent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Log-sum-exp merge of the nsplit partial records of output row bhq, element dim.
-__device__ inline float merge_dim(const DecodeArgs& a, size_t bhq, int dim, int nsplit) {
-    const float* ml = a.part_ml + bhq * a.splits * 2;
-    const float* acc = a.part_acc + bhq * a.splits * a.d;
+// Log-sum-exp merge of the nsplit partial records of row bhq0 + h, element dim.
+__device__ inline float merge_dim(const DecodeArgs& a, const RecMap& map, int h, int dim, int nsplit) {
+    const size_t r = map.r0 + static_cast<size_t>(h) * map.hs;
     float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, get_coherent(ml + 2 * s));
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, get_coherent(a.part_ml + (r + static_cast<size_t>(s) * map.ss) * 2));
     float L = 0.0f, A = 0.0f;
     for (int s = 0; s < nsplit; s++) {
-        const float w = fast_exp2(get_coherent(ml + 2 * s) - M);
-        L = fmaf(get_coherent(ml + 2 * s + 1), w, L);
-        A = fmaf(get_coherent(acc + static_cast<size_t>(s) * a.d + dim), w, A);
+        const size_t rec = r + static_cast<size_t>(s) * map.ss;
+        const float w = fast_exp2(get_coherent(a.part_ml + rec * 2) - M);
+        L = fmaf(get_coherent(a.part_ml + rec * 2 + 1), w, L);
+        A = fmaf(get_coherent(a.part_acc + rec * a.d + dim), w, A);
     }
     return A / L;
 }
 
-// One output element of a workgroup's result: the final value when the
-// sequence has one split, otherwise this split's partial record.
-__device__ __forceinline__ void store_result(const DecodeArgs& a, size_t bhq, int dim, int split, int nsplit,
-                                             float M, float L, float A) {
+// One output element of a workgroup's result, row bhq0 + h: the final value
+// when the sequence has one split, otherwise this split's partial record.
+__device__ __forceinline__ void store_result(const DecodeArgs& a, const RecMap& map, size_t bhq0, int h, int dim,
+                                             int split, int nsplit, float M, float L, float A) {
     if (nsplit == 1) {
-        a.out[bhq * a.d + dim] = A / L;
+        a.out[(bhq0 + h) * a.d + dim] = A / L;
     } else {
-        const size_t rec = bhq * a.splits + split;
+        const size_t rec = map.r0 + static_cast<size_t>(h) * map.hs + static_cast<size_t>(split) * map.ss;
         put_coherent(a.part_acc + rec * a.d + dim, A);
         if (dim == 0) {
             put_coherent(a.part_ml + rec * 2, M);
@@ -97,12 +148,17 @@ constexpr int kMergeSplits = 256;
 constexpr int kMergeMaxThreads = 512;
 constexpr int kCoherent = 16;  // buffer-load cache policy: sc1, device-coherent (as get_coherent)
 
-__device__ inline bool merge_group_fits(const DecodeArgs& a, int nheads, int nsplit) {
-    return nheads <= kMergeHeads && nsplit <= kMergeSplits && (a.d & 3) == 0 &&
-           static_cast<long>(nheads) * a.splits * a.d < (1L << 29) && blockDim.x <= kMergeMaxThreads;
+// Records spanned by the group's merge (relative to map.r0).
+__device__ __forceinline__ long merge_span(const RecMap& map, int nheads, int nsplit) {
+    return static_cast<long>(nheads - 1) * map.hs + static_cast<long>(nsplit - 1) * map.ss + 1;
 }
 
-__device__ inline void merge_group(const DecodeArgs& a, size_t bhq0, int nheads, int nsplit) {
+__device__ inline bool merge_group_fits(const DecodeArgs& a, const RecMap& map, int nheads, int nsplit) {
+    return nheads <= kMergeHeads && nsplit <= kMergeSplits && (a.d & 3) == 0 &&
+           merge_span(map, nheads, nsplit) * a.d < (1L << 29) && blockDim.x <= kMergeMaxThreads;
+}
+
+__device__ inline void merge_group(const DecodeArgs& a, const RecMap& map, size_t bhq0, int nheads, int nsplit) {
     __shared__ float s_w[kMergeHeads][kMergeSplits];  // m, then the weights
     __shared__ float s_L[kMergeHeads];
     union LOrPart {
@@ -115,10 +171,11 @@ __device__ inline void merge_group(const DecodeArgs& a, size_t bhq0, int nheads,
     const int lane = t & (kWave - 1);
     const int wave = t / kWave;
     const int nw = T / kWave;
-    const int S = a.splits;
     const int d = a.d;
-    const buf_rsrc mlr = make_rsrc(a.part_ml + bhq0 * S * 2, static_cast<unsigned>(nheads * S * 8));
-    const buf_rsrc accr = make_rsrc(a.part_acc + bhq0 * S * d, static_cast<unsigned>(nheads * S * d * 4));
+    const int hs = map.hs, ss = map.ss;
+    const unsigned span = static_cast<unsigned>(merge_span(map, nheads, nsplit));
+    const buf_rsrc mlr = make_rsrc(a.part_ml + map.r0 * 2, span * 8u);
+    const buf_rsrc accr = make_rsrc(a.part_acc + map.r0 * d, span * static_cast<unsigned>(d) * 4u);
 
     const int npairs = nheads * nsplit;  // <= 2048, so at most 8 per thread
 #pragma unroll
@@ -128,7 +185,7 @@ __device__ inline void merge_group(const DecodeArgs& a, size_t bhq0, int nheads,
             const int h = i / nsplit;
             const int sp = i - h * nsplit;
             typedef int v2i_t __attribute__((ext_vector_type(2)));
-            const v2i_t x = __builtin_amdgcn_raw_buffer_load_b64(mlr, (h * S + sp) * 8, 0, kCoherent);
+            const v2i_t x = __builtin_amdgcn_raw_buffer_load_b64(mlr, (h * hs + sp * ss) * 8, 0, kCoherent);
             s_w[h][sp] = __int_as_float(x.x);
             s_x.l[h][sp] = __int_as_float(x.y);
         }
@@ -156,14 +213,14 @@ __device__ inline void merge_group(const DecodeArgs& a, size_t bhq0, int nheads,
         const int j = item / ncols;
         const int c = item - j * ncols;
         const int h = c / cpr;
-        const int off0 = (h * S * d + 4 * (c - h * cpr)) * 4;
+        const int off0 = (h * hs * d + 4 * (c - h * cpr)) * 4;
         float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (int sp0 = j; sp0 < nsplit; sp0 += 16 * groups) {
             v4i_t v[16];
 #pragma unroll
             for (int k = 0; k < 16; k++) {
                 const int sp = sp0 + k * groups;
-                v[k] = sp < nsplit ? __builtin_amdgcn_raw_buffer_load_b128(accr, off0 + sp * d * 4, 0, kCoherent)
+                v[k] = sp < nsplit ? __builtin_amdgcn_raw_buffer_load_b128(accr, off0 + sp * ss * d * 4, 0, kCoherent)
                                    : v4i_t{0, 0, 0, 0};
             }
 #pragma unroll
@@ -201,10 +258,10 @@ __device__ inline void merge_group(const DecodeArgs& a, size_t bhq0, int nheads,
 }
 
 // Called by every thread of a workgroup after its store_result calls: counts
-// the split's arrival and, in the last workgroup of the sequence group, merges
-// the records of heads [bhq0, bhq0 + nheads).  s_last: one int of LDS.
-__device__ __forceinline__ void finish_split(const DecodeArgs& a, int unit, size_t bhq0, int nheads, int nsplit,
-                                             int* s_last) {
+// the split's arrival and, in the last workgroup of the work unit, merges the
+// records of rows [bhq0, bhq0 + nheads).  s_last: one int of LDS.
+__device__ __forceinline__ void finish_split(const DecodeArgs& a, int unit, const RecMap& map, size_t bhq0,
+                                             int nheads, int nsplit, int* s_last) {
     if (nsplit <= 1 || a.counters == nullptr) return;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's record stores have completed
     __syncthreads();
@@ -214,13 +271,13 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, int unit, size
     }
     __syncthreads();
     if (*s_last) {
-        if (merge_group_fits(a, nheads, nsplit)) {
-            merge_group(a, bhq0, nheads, nsplit);
+        if (merge_group_fits(a, map, nheads, nsplit)) {
+            merge_group(a, map, bhq0, nheads, nsplit);
         } else {
             for (int i = threadIdx.x; i < nheads * a.d; i += blockDim.x) {
                 const int h = i / a.d;
                 const int dim = i - h * a.d;
-                a.out[(bhq0 + h) * a.d + dim] = merge_dim(a, bhq0 + h, dim, nsplit);
+                a.out[(bhq0 + h) * a.d + dim] = merge_dim(a, map, h, dim, nsplit);
             }
         }
         if (threadIdx.x == 0)  // ready for the next launch

@@ -1,0 +1,107 @@
+"""Ragged batches under the device split schedule (per-sequence lengths on the
+device, num_splits = 0): the schedule kernel picks the chunk from the actual
+lengths and orders the work longest first, so every split of every sequence
+must be computed exactly once, merged right, and the arrival counters left at
+zero for the next launch.
+
+Parity as in test_gpu_decode: out[b, hq] = oracle kvq_ref_decode_f32 over the
+first length[b] tokens of kv head hq / G; 1e-4 abs + 1e-3 rel elementwise;
+appended int8 values and scales bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_close, make_problem
+import _gpu
+from _gpu import down, kvq, up
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def o():
+    return orc.get()
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def _ragged_lengths(rng, B, cap):
+    lengths = rng.integers(0, cap + 1, B).astype(np.int32)
+    edge = np.array([0, 1, cap, 129, 2, cap - 1], np.int32)[:B]
+    lengths[: len(edge)] = edge
+    return lengths
+
+
+@pytest.mark.parametrize("append", [False, True])
+@pytest.mark.parametrize("G,d", [(1, 128), (2, 64), (4, 128), (8, 128), (1, 256), (4, 32)])
+def test_schedule_ragged(o, G, d, append):
+    """VALU (G = 1, 2; d 32..256) and matrix-core (G = 4, 8 at d = 128) kernels."""
+    rng = np.random.default_rng(1000 * G + d + append)
+    B, Hkv, cap = 24, 2, 2048
+    lengths = _ragged_lengths(rng, B, cap)
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, dist="student_t", lengths=lengths)
+    kn = vn = None
+    if append:
+        kn = rng.standard_t(4, (B, Hkv, d)).astype(np.float32)
+        vn = rng.standard_t(4, (B, Hkv, d)).astype(np.float32)
+    got, gk, gv, gks, gvs = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths,
+                                         k_new=kn, v_new=vn)
+    if append:
+        o.append(kn, vn, p["k"], p["v"], p["ks"], p["vs"], positions=lengths - 1)
+        assert np.array_equal(gk, p["k"]) and np.array_equal(gv, p["v"]), "appended int8 differs"
+        assert np.array_equal(_bits(gks), _bits(p["ks"])) and np.array_equal(_bits(gvs), _bits(p["vs"]))
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert_close(got, want, what=f"scheduled G={G} d={d} append={append}")
+
+
+@pytest.mark.parametrize("G", [1, 4])
+def test_schedule_one_long_many_short(o, G):
+    """One long sequence among many short ones: the chunk shrinks to the
+    batch's mean, so the long one is cut into many splits (more than one
+    merge pass can hold for G = 1) while the short ones run whole."""
+    rng = np.random.default_rng(55 + G)
+    B, Hkv, cap, d = 96, 1, 20000, 128
+    lengths = rng.integers(1, 40, B).astype(np.int32)
+    lengths[17] = cap
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, lengths=lengths)
+    got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)[0]
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert_close(got, want, what=f"one long, many short, G={G}")
+
+
+def test_schedule_large_batch(o):
+    """More sequences than the schedule kernel's threads (several scan rounds)."""
+    rng = np.random.default_rng(3)
+    B, Hkv, G, cap, d = 2500, 1, 2, 96, 64
+    lengths = rng.integers(0, cap + 1, B).astype(np.int32)
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, lengths=lengths)
+    got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)[0]
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert_close(got, want, what="large batch")
+
+
+@pytest.mark.parametrize("G", [1, 8])
+def test_schedule_repeated_launches_new_lengths(o, G):
+    """One workspace, several launches whose device lengths change in between
+    (the schedule is recomputed each launch; counters must be back at zero)."""
+    rng = np.random.default_rng(90 + G)
+    B, Hkv, cap, d = 12, 2, 1500, 128
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows)
+    gq, gk, gv, gks, gvs = up(p["q"]), up(p["k"]), up(p["v"]), up(p["ks"]), up(p["vs"])
+    glen = torch.zeros(B, dtype=torch.int32, device=_gpu.dev())
+    out = _gpu.poisoned(p["q"].shape)
+    dec = kvq.Decoder(gq, gk, gv, gks, gvs, out, lengths=glen, max_seq_len=cap)
+    for it in range(4):
+        lengths = rng.integers(0, cap + 1, B).astype(np.int32)
+        if it == 1:
+            lengths[:] = cap
+        glen.copy_(torch.from_numpy(lengths))
+        out.fill_(float("nan"))
+        dec()
+        torch.cuda.synchronize()
+        want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+        assert_close(down(out), want, what=f"launch {it}")
