@@ -6,7 +6,7 @@
 // kept in log2 units (softmax_scale * log2 e folded into one multiplier) so
 // every exponential is one v_exp_f32.
 //
-// decode_fast<D, SG>: one workgroup (4 waves) per (sequence split, batch,
+// decode_fast<D, SG>: one workgroup (8 waves) per (sequence split, batch,
 //   kv head, group of SG query heads).  A token's D-byte K row is read by D/16
 //   lanes with one 16-byte load each, so one wave load covers 64*16 contiguous
 //   bytes (several whole rows).  Each lane dequantises its 16 bytes in
@@ -22,8 +22,9 @@
 //   arrival counter) merges the records with a log-sum-exp reduction, so the
 //   whole decode is a single kernel.  Without counters (caller scratch of
 //   unknown contents) merge_kernel does the merge instead.
-//   Optionally the workgroup owning a sequence's last token first quantises that
-//   token from fp32 (append) and attends to it from registers.
+//   Optionally wave 0 of the workgroup owning a sequence's last token
+//   quantises that token from fp32 (append) after its tiles, with no
+//   workgroup barrier, and attends to it from registers.
 //
 // decode_generic: any head dim up to KVQ_MAX_HEAD_DIM and any alignment; one
 //   wave per (split, batch, query head), q and the accumulators in LDS.  It is
@@ -43,13 +44,15 @@ namespace {
 constexpr int kFastWaves = KVQ_FAST_WAVES;  // waves per workgroup
 
 // Tile geometry: D/16 lanes share a token (16 bytes each); U tokens per lane
-// group per loop iteration (fewer when SG query heads already hold 2*16*SG
-// registers of q and accumulators).
+// group per loop iteration.  U = 2 keeps ~32 KB of K/V loads in flight per CU
+// (8 waves x 2 x 2 KB), which measured fastest on MI355X: at U = 4 (64 KB) the
+// same kernel streams ~4% slower, at U = 8 ~15% slower, at U = 1 too little
+// is in flight.
 template <int D, int SG>
 struct FastGeom {
     static constexpr int LPT = D / 16;                // lanes per token
     static constexpr int TPL = kWave / LPT;           // tokens per wave load
-    static constexpr int U = SG >= 4 ? 2 : 4;         // tokens per lane group per iteration
+    static constexpr int U = 2;                       // tokens per lane group per iteration
     // Software pipelining (next tile's loads in flight during compute) pays
     // for SG = 4; at SG <= 2 the extra registers cost more than it hides.
     static constexpr bool PIPE = SG >= 4;
@@ -116,12 +119,9 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     using Geo = FastGeom<D, SG>;
     constexpr int LPT = Geo::LPT;
     constexpr int U = Geo::U;
-    constexpr int NT = kFastWaves * kWave;
-    constexpr int NE = (2 * D + NT - 1) / NT;  // appended K+V elements per thread
+    constexpr int NE = (2 * D + kWave - 1) / kWave;  // appended K+V elements per lane of wave 0
     __shared__ float s_ml[kFastWaves][SG][2];
     __shared__ float s_acc[kFastWaves][SG][D];
-    __shared__ float s_amax[2][kFastWaves];
-    __shared__ float s_newscale[2];
     __shared__ __align__(16) int s_newq[2][D / 4];  // appended K and V rows, packed int8
     __shared__ int s_last;
 
@@ -153,14 +153,14 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     const bool app = (a.k_new != nullptr) && (t1 == len);
     const int tend = app ? t1 - 1 : t1;  // tokens read from the cache
 
-    // Fused append, part 1: fetch the new token (element e of the K row then
-    // the V row per thread) now, so the loads overlap the main loop.
+    // Fused append, part 1: wave 0 fetches the new token (element e = lane +
+    // 64 j of the K row then the V row) first, so the loads overlap the rest.
     float xnew[NE];
 #pragma unroll
     for (int j = 0; j < NE; j++) {
-        const int e = threadIdx.x + j * NT;
+        const int e = lane + j * kWave;
         xnew[j] = 0.0f;
-        if (app && e < 2 * D)
+        if (app && wave == 0 && e < 2 * D)
             xnew[j] = (e < D ? a.k_new : a.v_new)[static_cast<size_t>(bh) * D + (e < D ? e : e - D)];
     }
 
@@ -254,62 +254,43 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
         }
     }
 
-    if (app) {
-        // Fused append, part 2: per-row max|x| over the workgroup, the scale,
-        // one quantised element per thread (same rule and bits as
-        // append_kernel), rows handed over through LDS.
+    if (app && wave == 0) {
+        // Fused append, part 2 (wave 0 alone, no workgroup barrier): per-row
+        // max|x|, the scale, the quantised elements (same rule and bits as
+        // append_kernel) into LDS, read back in the attend layout; one store
+        // of the token per kv head, and lane group 0 attends to it.
         float mk = 0.0f, mv = 0.0f;
 #pragma unroll
         for (int j = 0; j < NE; j++) {
-            const int e = threadIdx.x + j * NT;
+            const int e = lane + j * kWave;
             if (e < D) mk = fmaxf(mk, fabsf(xnew[j]));
             else if (e < 2 * D) mv = fmaxf(mv, fabsf(xnew[j]));
         }
-        mk = wave_max(mk);
-        mv = wave_max(mv);
-        if (lane == 0) {
-            s_amax[0][wave] = mk;
-            s_amax[1][wave] = mv;
-        }
-        __syncthreads();
-        float ak = 0.0f, av = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kFastWaves; w++) {
-            ak = fmaxf(ak, s_amax[0][w]);
-            av = fmaxf(av, s_amax[1][w]);
-        }
-        const float sk = quant_scale(ak), sv = quant_scale(av);
+        const float sk = quant_scale(wave_max(mk)), sv = quant_scale(wave_max(mv));
 #pragma unroll
         for (int j = 0; j < NE; j++) {
-            const int e = threadIdx.x + j * NT;
+            const int e = lane + j * kWave;
             if (e < 2 * D) {
                 const int row = e < D ? 0 : 1;
                 reinterpret_cast<int8_t*>(s_newq[row])[e - row * D] =
                     static_cast<int8_t>(quant_one(xnew[j], row ? sv : sk));
             }
         }
-        if (threadIdx.x == 0) {
-            s_newscale[0] = sk;
-            s_newscale[1] = sv;
-        }
-        __syncthreads();
-        if (wave == 0) {
-            int4 kk1[1], vv1[1];
-            kk1[0] = *reinterpret_cast<const int4*>(&s_newq[0][ds * 4]);
-            vv1[0] = *reinterpret_cast<const int4*>(&s_newq[1][ds * 4]);
-            const float sk1[1] = {s_newscale[0]}, sv1[1] = {s_newscale[1]};
-            const int tnew = len - 1;
-            if (sgi == 0 && tg == 0) {  // one store of the token per kv head
-                *reinterpret_cast<int4*>(a.k + (row0 + tnew) * D + ds * 16) = kk1[0];
-                *reinterpret_cast<int4*>(a.v + (row0 + tnew) * D + ds * 16) = vv1[0];
-                if (ds == 0) {
-                    a.ks[row0 + tnew] = sk1[0];
-                    a.vs[row0 + tnew] = sv1[0];
-                }
+        int4 kk1[1], vv1[1];
+        kk1[0] = *reinterpret_cast<const int4*>(&s_newq[0][ds * 4]);
+        vv1[0] = *reinterpret_cast<const int4*>(&s_newq[1][ds * 4]);
+        const float sk1[1] = {sk}, sv1[1] = {sv};
+        const int tnew = len - 1;
+        if (sgi == 0 && tg == 0) {
+            *reinterpret_cast<int4*>(a.k + (row0 + tnew) * D + ds * 16) = kk1[0];
+            *reinterpret_cast<int4*>(a.v + (row0 + tnew) * D + ds * 16) = vv1[0];
+            if (ds == 0) {
+                a.ks[row0 + tnew] = sk;
+                a.vs[row0 + tnew] = sv;
             }
-            const bool ok1[1] = {tg == 0};
-            attend<SG, 1, LPT>(qr, kk1, vv1, sk1, sv1, ok1, a.scale_log2, m, l, acc);
         }
+        const bool ok1[1] = {tg == 0};
+        attend<SG, 1, LPT>(qr, kk1, vv1, sk1, sv1, ok1, a.scale_log2, m, l, acc);
     }
 
     // Merge the lane groups of this wave (lanes that share ds).

@@ -32,9 +32,9 @@
 //   The token order of a lane group's k-slots (4g..4g+3, 16+4g..16+4g+3)
 //   matches where the QK C layout left that lane's probabilities, so P needs
 //   no data movement.
-// * fused append: the new token is quantised by the whole workgroup before
-//   each wave's last tile (its fp32 loads were issued at kernel start) and
-//   substituted from LDS where the last tile reads token length-1.
+// * fused append: the new token is quantised by the one wave whose last tile
+//   holds token length-1 (its fp32 loads were issued at kernel start) and
+//   substituted from LDS into that tile.
 #include <math.h>
 
 #include "kvq_device.hpp"
@@ -83,8 +83,7 @@ template <int G>
 __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma(
     const DecodeArgs a) {
     static_assert(G == 4 || G == 8, "heads per workgroup");
-    constexpr int NT = kMWaves * kWave;
-    static_assert(NT == 2 * kMD, "the fused append gives one K or V element to each thread");
+    static_assert(2 * kMD == 4 * kWave, "the fused append gives 4 K/V elements to each lane of a wave");
     // V tile buffers during the tile loop; the waves' results afterwards.
     union TileOrResult {
         int8_t v[kMWaves][2][kMTile * kMD];
@@ -95,8 +94,6 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     auto& s_acc = s_u.acc;
     __shared__ float s_ml[kMWaves][G][2];
     __shared__ __align__(16) int8_t s_newq[2][kMD];
-    __shared__ float s_newscale[2];
-    __shared__ float s_amax[2][2];
     __shared__ int s_last;
 
     const int lane = threadIdx.x & (kWave - 1);
@@ -128,10 +125,15 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     const int tnew = len - 1;
     const size_t row0 = static_cast<size_t>(bh) * a.cap;
 
-    // Fused append, part 1: this thread's element of the new K (threads
-    // 0..127) or V (128..255) row, fetched early.
-    float xnew = 0.0f;
-    if (app) xnew = (threadIdx.x < kMD ? a.k_new : a.v_new)[static_cast<size_t>(bh) * kMD + (threadIdx.x & (kMD - 1))];
+    // Fused append: the wave whose tiles include token len-1 (wave w's tiles
+    // start at t0 + 32 w + 128 i) quantises the new token on its own; its fp32
+    // row is fetched first (element lane + 64 j: j < 2 of K, j >= 2 of V).
+    const bool own_new = app && ((tnew - t0) / kMTile) % kMWaves == wave;
+    float xnew[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        xnew[j] = own_new ? (j < 2 ? a.k_new : a.v_new)[static_cast<size_t>(bh) * kMD + ((lane + kWave * j) & (kMD - 1))]
+                          : 0.0f;
 
     // q of head (r % G) as int8 limbs in the QK B operand layout:
     // qb[j][limb] holds dims 64j + 16g + [0,16).
@@ -151,34 +153,40 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             }
         }
     }
-    float qmax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) qmax = fmaxf(qmax, fabsf(qv[i]));
-    qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
-    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
-    int qexp = 0;
-    frexpf(qmax, &qexp);  // qmax < 2^qexp
-    const int E = qmax > 0.0f ? min(max(22 - qexp, -100), 126) : 0;
-    const float qdeq = ldexpf(1.0f, -E);
+    // The limbs are formed after the first tile's loads are issued (their
+    // latency overlaps this work); qs turns an integer dot into a score in
+    // log2 units (after x k_scale).
     i32x4 qb[2][3];
+    float qs = 0.0f;
+    auto prepare_q = [&]() {
+        float qmax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        int limb[3][16];
+        for (int i = 0; i < 32; i++) qmax = fmaxf(qmax, fabsf(qv[i]));
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+        int qexp = 0;
+        frexpf(qmax, &qexp);  // qmax < 2^qexp
+        const int E = qmax > 0.0f ? min(max(22 - qexp, -100), 126) : 0;
+        qs = ldexpf(1.0f, -E) * a.scale_log2;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int Q = static_cast<int>(__builtin_rintf(ldexpf(qv[16 * j + i], E)));
-            const int l2 = ((Q + 128) & 255) - 128;
-            const int Q1 = (Q - l2) >> 8;
-            const int l1 = ((Q1 + 128) & 255) - 128;
-            limb[0][i] = (Q1 - l1) >> 8;
-            limb[1][i] = l1;
-            limb[2][i] = l2;
+        for (int j = 0; j < 2; j++) {
+            int limb[3][16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int Q = static_cast<int>(__builtin_rintf(ldexpf(qv[16 * j + i], E)));
+                const int l2 = ((Q + 128) & 255) - 128;
+                const int Q1 = (Q - l2) >> 8;
+                const int l1 = ((Q1 + 128) & 255) - 128;
+                limb[0][i] = (Q1 - l1) >> 8;
+                limb[1][i] = l1;
+                limb[2][i] = l2;
+            }
+#pragma unroll
+            for (int lb = 0; lb < 3; lb++)
+                qb[j][lb] = i32x4{pack_bytes(&limb[lb][0]), pack_bytes(&limb[lb][4]), pack_bytes(&limb[lb][8]),
+                                  pack_bytes(&limb[lb][12])};
         }
-#pragma unroll
-        for (int lb = 0; lb < 3; lb++)
-            qb[j][lb] = i32x4{pack_bytes(&limb[lb][0]), pack_bytes(&limb[lb][4]), pack_bytes(&limb[lb][8]),
-                              pack_bytes(&limb[lb][12])};
-    }
+    };
 
     // Online-softmax state of head hrow (identical in every lane of that
     // row): the score max m (log2 units), the denominator lsum, and vref, the
@@ -190,7 +198,6 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int c = 0; c < 8; c++) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const bool lo_row = ((r / G) & 1) != 0;
-    const float qs = qdeq * a.scale_log2;  // integer dot -> score in log2 units (after x k_scale)
 
     // This (batch, kv head)'s cache rows as buffer resources: tile loads add a
     // fixed per-lane offset to a wave-uniform tile offset, and a tail tile's
@@ -207,25 +214,28 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     const int h2 = lane & 1;
     const int vrow = rr < 4 ? 4 * g + rr : 16 + 4 * g + (rr - 4);
 
-    // Fused append, part 2 (whole workgroup): per-row max|x| (waves 0,1: K;
-    // 2,3: V), the scale, one element per thread -- same rule and bits as
-    // append_kernel.  The row lands in LDS for the final tile and in the cache
-    // for later steps.
-    auto append_part2 = [&]() {
-        const float am = wave_max(fabsf(xnew));
-        if (lane == 0) s_amax[wave >> 1][wave & 1] = am;
-        __syncthreads();
-        const int row = threadIdx.x / kMD;
-        const int col = threadIdx.x & (kMD - 1);
-        const float scale = quant_scale(fmaxf(s_amax[row][0], s_amax[row][1]));
-        const int qn = quant_one(xnew, scale);
-        s_newq[row][col] = static_cast<int8_t>(qn);
-        if (col == 0) s_newscale[row] = scale;
+    // Fused append, part 2 (the owning wave, no workgroup barrier): per-row
+    // max|x|, the scale, the quantised elements -- same rule and bits as
+    // append_kernel.  The rows land in LDS for the final tile and in the cache
+    // for later steps (once per kv head).
+    float newks = 0.0f, newvs = 0.0f;
+    auto append_new = [&]() {
+        newks = quant_scale(wave_max(fmaxf(fabsf(xnew[0]), fabsf(xnew[1]))));
+        newvs = quant_scale(wave_max(fmaxf(fabsf(xnew[2]), fabsf(xnew[3]))));
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            s_newq[j >> 1][lane + kWave * (j & 1)] = static_cast<int8_t>(quant_one(xnew[j], j < 2 ? newks : newvs));
         if (sgi == 0) {
-            (row ? a.v : a.k)[(row0 + tnew) * kMD + col] = static_cast<int8_t>(qn);
-            if (col == 0) (row ? a.vs : a.ks)[row0 + tnew] = scale;
+            if (lane < 16) {
+                const int row = lane >> 3, piece = lane & 7;
+                *reinterpret_cast<int4*>((row ? a.v : a.k) + (row0 + tnew) * kMD + 16 * piece) =
+                    *reinterpret_cast<const int4*>(&s_newq[row][16 * piece]);
+            }
+            if (lane == 0) {
+                a.ks[row0 + tnew] = newks;
+                a.vs[row0 + tnew] = newvs;
+            }
         }
-        __syncthreads();
     };
 
     // One tile's global data in registers: K sub-tiles (A operand of QK), the
@@ -292,8 +302,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
             for (int i = 0; i < 4; i++)
                 if (base + 16 * s + 4 * g + i == tnew) {
-                    T.ks[s][i] = s_newscale[0];
-                    T.vs[s][i] = s_newscale[1];
+                    T.ks[s][i] = newks;
+                    T.vs[s][i] = newvs;
                 }
         }
         const int rw = tnew - base;
@@ -391,9 +401,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // Software-pipelined tile loop: tile i+1's global loads are in flight
     // while tile i is computed; its V rows go to LDS buffer (i+1) % 2 at the
     // end of the iteration.  Two register tiles alternate (the loop body is
-    // written out twice), so no tile is copied.  The fused append runs before
-    // each wave's last tile (a workgroup barrier, so waves without tiles join
-    // it too).
+    // written out twice), so no tile is copied.
     Tile ta, tb;
     auto inner = [&](Tile& T, Tile& N, int it) {  // any tile but the last
         load_tile(N, it + 1);
@@ -402,6 +410,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     };
     if (ntiles > 0) {
         load_tile(ta, 0);
+        prepare_q();
         stage_v(ta, s_v[wave][0]);
         int it = 0;
         for (; it + 2 < ntiles; it += 2) {
@@ -415,13 +424,12 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         }
         const int base = wbase + it * kMBStep;
         int8_t* vt = s_v[wave][it & 1];
-        if (app) {
-            append_part2();
+        if (own_new) {
+            append_new();
             substitute_new(ta, base, vt);
         }
         compute(ta, base, vt, true);
     }
-    if (ntiles == 0 && app) append_part2();
 
     // Wave results to LDS: the softmax sum over the 4 lane groups, and the
     // accumulator in output units (relative to the score max m).
