@@ -11,8 +11,10 @@ Timing protocol:
   * inputs resident in HBM; the caches rotate over R replicas with
     R * KV_bytes >= 512 MiB (R >= 3) so steps read HBM, not the 256 MB
     Infinity Cache; a cache-warm single-replica figure is reported separately;
-  * W untimed warm-up steps, then exactly K steps between two HIP events on
-    the launch stream, synchronised on both sides -> ms_per_step, value;
+  * W untimed warm-up steps, then more untimed steps until --settle-ms of
+    wall time has passed (sustained load first, so clocks and power state
+    are at steady state), then exactly K steps between two HIP events on the
+    launch stream, synchronised on both sides -> ms_per_step, value;
   * every step is exactly one launch of the decode kernel, so the timed
     region / K is that kernel's average duration -> roofline.achieved; a
     second pass brackets every launch with its own events (reported as
@@ -44,9 +46,12 @@ METRIC = "KV-cache read GB/s (% HBM peak) + us/decode step at B8 H32 d128 L4096"
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=300)
-    ap.add_argument("--warmup", type=int, default=100,
-                    help="untimed steps first (the GPU needs ~1 ms of load to reach steady clocks)")
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=2000, help="untimed steps first")
+    ap.add_argument("--settle-ms", type=float, default=200.0,
+                    help="after the warm-up steps, keep launching untimed steps until this much wall "
+                         "time has passed since the warm-up began (MI355X runs this kernel ~15%% slower "
+                         "during its first ~20 ms of sustained load than in steady state)")
     ap.add_argument("--config", default="cfg1", help="cfg0..cfg4 (default cfg1, the headline)")
     ap.add_argument("--splits", type=int, default=0, help="splits per sequence (0 = library choice)")
     ap.add_argument("--replicas", type=int, default=0, help="cache replicas (0 = enough for 512 MiB, >= 3)")
@@ -129,16 +134,27 @@ def main():
             for p, o in zip(reps, outs)]
     torch.cuda.synchronize()
 
+    # Launches go to the current stream by its raw handle: one foreign call
+    # per step, so host work between launches stays small (heavier per-launch
+    # host work measurably slowed the running kernels on MI355X).
+    sh = stream.cuda_stream
+    t_warm = time.perf_counter()
     for i in range(args.warmup):
-        decs[i % R]()
+        decs[i % R](sh)
     torch.cuda.synchronize()
+    settle = 0
+    while (time.perf_counter() - t_warm) * 1e3 < args.settle_ms:
+        for _ in range(50):
+            decs[(args.warmup + settle) % R](sh)
+            settle += 1
+        torch.cuda.synchronize()
 
     # Pass 1: K steps between two events (the contract's timed region).
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream)
     for i in range(args.steps):
-        decs[i % R]()
+        decs[i % R](sh)
     e1.record(stream)
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
@@ -148,7 +164,7 @@ def main():
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n2)]
     for i, (a, b) in enumerate(ev):
         a.record(stream)
-        decs[i % R]()
+        decs[i % R](sh)
         b.record(stream)
     torch.cuda.synchronize()
     kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
@@ -156,10 +172,10 @@ def main():
     # Pass 3: cache-warm (single replica, no rotation), labelled separately.
     w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for _ in range(5):
-        decs[0]()
+        decs[0](sh)
     w0.record(stream)
     for _ in range(n2):
-        decs[0]()
+        decs[0](sh)
     w1.record(stream)
     torch.cuda.synchronize()
     warm_ms = w0.elapsed_time(w1) / n2
@@ -192,6 +208,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_steps": settle,
         "ms_per_step": round(ms_per_step, 6),
         "us_per_step": round(ms_per_step * 1e3, 3),
         "pct_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),

@@ -206,11 +206,16 @@ class Decoder:
                                     softmax_scale, num_splits, k_new, v_new)
         self.ws = new_workspace(self.params, q.device, stream)
         self.ws_bytes = workspace_size(self.params)
+        # Launch arguments resolved once: a step costs one foreign call.
+        self._launch = lib().kvq_decode_launch
+        self._args = (ctypes.byref(self.params), _ptr(self.ws), self.ws_bytes)
 
     def __call__(self, stream=None) -> None:
-        _check("kvq_decode_launch",
-               lib().kvq_decode_launch(ctypes.byref(self.params), _ptr(self.ws), self.ws_bytes,
-                                       _stream(stream)))
+        """Launch on `stream` (a torch stream or a raw hipStream_t handle;
+        default: torch's current stream)."""
+        code = self._launch(*self._args, stream if isinstance(stream, int) else _stream(stream))
+        if code != HIP_SUCCESS:
+            raise KvqError("kvq_decode_launch", code)
 
 
 def decode(q, k_cache, v_cache, k_scale, v_scale, lengths=None, max_seq_len=0, softmax_scale=0.0,
