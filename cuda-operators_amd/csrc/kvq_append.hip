@@ -26,9 +26,10 @@ __global__ __launch_bounds__(2 * kWave) void append_kernel(const float* k_new, c
                                                            int8_t* k, int8_t* v, float* ks, float* vs,
                                                            const int32_t* positions, int uniform_pos,
                                                            int from_lengths, int max_len, int Hkv, int cap,
-                                                           int d) {
+                                                           int d, const PageMap pages) {
     const int bh = blockIdx.x;
     const int b = bh / Hkv;
+    const int kvh = bh - b * Hkv;
     int pos;
     if (positions == nullptr) pos = uniform_pos;
     else if (from_lengths) pos = min(max(positions[b], 0), max_len) - 1;
@@ -36,7 +37,7 @@ __global__ __launch_bounds__(2 * kWave) void append_kernel(const float* k_new, c
     if (pos < 0 || pos >= cap) return;
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
-    const size_t tok = static_cast<size_t>(bh) * cap + pos;
+    const size_t tok = cache_row(pages, Hkv, cap, b, kvh, pos);
     if (wave == 0) quantize_row_wave(k_new + static_cast<size_t>(bh) * d, d, k + tok * d, ks + tok, lane);
     else quantize_row_wave(v_new + static_cast<size_t>(bh) * d, d, v + tok * d, vs + tok, lane);
 }
@@ -63,10 +64,11 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(uint8_t* p, size_t bytes
 
 hipError_t launch_append(const float* k_new, const float* v_new, int8_t* k, int8_t* v, float* ks,
                          float* vs, const int32_t* positions, int uniform_pos, bool from_lengths,
-                         int B, int Hkv, int max_len, int cap, int d, hipStream_t stream) {
+                         int B, int Hkv, int max_len, int cap, int d, const PageMap& pages,
+                         hipStream_t stream) {
     hipLaunchKernelGGL(append_kernel, dim3(static_cast<unsigned>(B * Hkv)), dim3(2 * kWave), 0, stream,
                        k_new, v_new, k, v, ks, vs, positions, uniform_pos, from_lengths ? 1 : 0, max_len,
-                       Hkv, cap, d);
+                       Hkv, cap, d, pages);
     return hipGetLastError();
 }
 

@@ -50,21 +50,27 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // aligned: q, caches and new rows are 16-byte aligned (vector loads);
 // quads: the matrix-core kernel's layout needs hold (scale arrays 16-byte
 // aligned, capacity a multiple of 4 and below 2^24);
+// page: tokens per page of a paged cache (0: contiguous); a tuned kernel runs
+// a paged cache only when no wave tile straddles a page;
 // ragged: per-sequence lengths on the device;
 // max_splits bounds the splits (scratch capacity of the reference ABI);
 // fused selects the arrival-counter merge (workspace holds counters).
-DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, bool quads, bool ragged,
-                     int requested, int max_splits, bool fused) {
+DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, bool quads, int page,
+                     bool ragged, int requested, int max_splits, bool fused) {
     DecodePlan p{};
     const int G = Hq / Hkv;
     const int sg_m = kvq::mfma_heads_per_group(G, d);
     const int sg_v = kvq::fast_heads_per_group(G);
+    const bool pow2 = page > 0 && (page & (page - 1)) == 0;
+    const int wave_tokens = kvq::fast_wave_tokens(d, sg_v);
+    const bool valu_pages = page == 0 || (pow2 && wave_tokens > 0 && page % wave_tokens == 0);
+    const bool mfma_pages = page == 0 || (pow2 && page % 32 == 0 && page < (1 << 24));
     int tile = 0;
-    if (aligned && quads && sg_m > 0) {
+    if (aligned && quads && mfma_pages && sg_m > 0) {
         p.kernel = kvq::Kernel::Mfma;
         p.sg = sg_m;
         tile = kvq::mfma_tile_tokens();
-    } else if (aligned && kvq::fast_tile_tokens(d, sg_v) > 0) {
+    } else if (aligned && valu_pages && kvq::fast_tile_tokens(d, sg_v) > 0) {
         p.kernel = kvq::Kernel::Valu;
         p.sg = sg_v;
         tile = kvq::fast_tile_tokens(d, sg_v);
@@ -101,8 +107,11 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
         splits = std::min<long>(requested, max_len);
         splits = std::min<long>(splits, std::max(max_splits, 1));
         chunk = static_cast<int>((max_len + splits - 1) / splits);
-        // Matrix-core tiles start at multiples of 4 tokens (aligned scale quads).
-        if (p.kernel == kvq::Kernel::Mfma && splits > 1) chunk = static_cast<int>(round_up(static_cast<size_t>(chunk), 4));
+        // Tuned kernels get chunks of whole workgroup tiles: matrix-core tiles
+        // must start at multiples of 4 tokens (aligned scale quads), and in a
+        // paged cache no wave tile may straddle a page.  So fewer splits than
+        // requested may run.
+        if (p.fast && splits > 1) chunk = static_cast<int>(round_up(static_cast<size_t>(chunk), gran));
     } else {
         const long target = p.kernel == kvq::Kernel::Mfma ? kTargetWorkgroupsMfma : kTargetWorkgroupsValu;
         splits = (target + units - 1) / units;
@@ -174,7 +183,7 @@ hipError_t reference_launch(const float* Q, const int8_t* K, const int8_t* V, co
     DecodeArgs a = reference_args(Q, K, V, ks, vs, out, H, N, d);
     // S holds H*N floats; a split needs (d + 2) floats per head.
     const int max_splits = std::max(1, N / (d + 2));
-    const DecodePlan p = make_plan(1, H, H, d, N, reference_aligned(Q, K, V, d), false, false, 0, max_splits, false);
+    const DecodePlan p = make_plan(1, H, H, d, N, reference_aligned(Q, K, V, d), false, 0, false, 0, max_splits, false);
     a.splits = p.splits;
     a.chunk = p.chunk;
     a.nsg = p.nsg;
@@ -250,7 +259,44 @@ bool decode_mfma_layout(const kvq_decode_params* p) {
 
 DecodePlan decode_plan(const kvq_decode_params* p) {
     return make_plan(p->batch, p->num_q_heads, p->num_kv_heads, p->head_dim, decode_max_len(p),
-                     decode_aligned(p), decode_mfma_layout(p), p->lengths != nullptr, p->num_splits, INT_MAX, true);
+                     decode_aligned(p), decode_mfma_layout(p), 0, p->lengths != nullptr, p->num_splits, INT_MAX,
+                     true);
+}
+
+bool paged_params_ok(const kvq_paged_decode_params* p) {
+    if (!p) return false;
+    if (p->batch <= 0 || p->num_q_heads <= 0 || p->num_kv_heads <= 0) return false;
+    if (p->num_q_heads % p->num_kv_heads != 0) return false;
+    if (p->head_dim <= 0 || p->head_dim > KVQ_MAX_HEAD_DIM) return false;
+    if (p->page_size <= 0 || p->num_pages <= 0 || p->max_pages_per_seq <= 0) return false;
+    const long long cap = static_cast<long long>(p->max_pages_per_seq) * p->page_size;
+    if (cap > INT_MAX || p->max_seq_len < 0 || p->max_seq_len > cap || p->num_splits < 0) return false;
+    if (!p->block_table || !p->lengths || !p->q || !p->k_pages || !p->v_pages || !p->k_scale_pages ||
+        !p->v_scale_pages || !p->out)
+        return false;
+    if ((p->k_new == nullptr) != (p->v_new == nullptr)) return false;
+    if (static_cast<long long>(p->batch) * p->num_q_heads > INT_MAX / 4) return false;
+    if (static_cast<long long>(p->batch) * p->max_pages_per_seq > INT_MAX) return false;
+    return true;
+}
+
+int paged_cap(const kvq_paged_decode_params* p) { return p->max_pages_per_seq * p->page_size; }
+int paged_max_len(const kvq_paged_decode_params* p) { return p->max_seq_len > 0 ? p->max_seq_len : paged_cap(p); }
+
+kvq::PageMap page_map(const int32_t* table, int size, int max_pages, int num_pages) {
+    int shift = -1;
+    if ((size & (size - 1)) == 0)
+        for (shift = 0; (1 << shift) < size; shift++) {
+        }
+    return kvq::PageMap{table, size, max_pages, num_pages, shift};
+}
+
+DecodePlan paged_plan(const kvq_paged_decode_params* p) {
+    const bool aligned = aligned16(p->q) && aligned16(p->k_pages) && aligned16(p->v_pages) &&
+                         (p->head_dim % 16) == 0 && (!p->k_new || (aligned16(p->k_new) && aligned16(p->v_new)));
+    const bool quads = aligned16(p->k_scale_pages) && aligned16(p->v_scale_pages);
+    return make_plan(p->batch, p->num_q_heads, p->num_kv_heads, p->head_dim, paged_max_len(p), aligned, quads,
+                     p->page_size, true, p->num_splits, INT_MAX, true);
 }
 
 }  // namespace
@@ -272,7 +318,7 @@ void solve(const float* Q, const int8_t* K_int8, const int8_t* V_int8, const flo
     }
     DecodeArgs a = reference_args(Q, K_int8, V_int8, k_scale, v_scale, output, num_heads, seq_len, head_dim);
     const DecodePlan p = make_plan(1, num_heads, num_heads, head_dim, seq_len,
-                                   reference_aligned(Q, K_int8, V_int8, head_dim), false, false, 0, INT_MAX, true);
+                                   reference_aligned(Q, K_int8, V_int8, head_dim), false, 0, false, 0, INT_MAX, true);
     a.splits = p.splits;
     a.chunk = p.chunk;
     a.nsg = p.nsg;
@@ -348,7 +394,7 @@ hipError_t kvq_append_launch(const kvq_append_params* p, hipStream_t stream) {
     if (static_cast<long long>(p->batch) * p->num_kv_heads > INT_MAX) return hipErrorInvalidValue;
     return kvq::launch_append(p->k_new, p->v_new, p->k_cache, p->v_cache, p->k_scale, p->v_scale, p->positions,
                               p->uniform_position, false, p->batch, p->num_kv_heads, p->capacity,
-                              p->capacity, p->head_dim, stream);
+                              p->capacity, p->head_dim, kvq::PageMap{nullptr, 0, 0, 0, -1}, stream);
 }
 
 hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, int8_t* q, float* scale,
@@ -356,6 +402,60 @@ hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, 
     if (rows < 0 || head_dim <= 0 || head_dim > KVQ_MAX_HEAD_DIM) return hipErrorInvalidValue;
     if (rows > 0 && (!x || !q || !scale)) return hipErrorInvalidValue;
     return kvq::launch_quantize_rows(x, rows, head_dim, q, scale, stream);
+}
+
+size_t kvq_paged_decode_workspace_size(const kvq_paged_decode_params* p) {
+    if (!paged_params_ok(p)) return 0;
+    return plan_bytes(paged_plan(p));
+}
+
+hipError_t kvq_paged_decode_launch(const kvq_paged_decode_params* p, void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream) {
+    if (!paged_params_ok(p)) return hipErrorInvalidValue;
+    const DecodePlan plan = paged_plan(p);
+    const size_t need = plan_bytes(plan);
+    if (need > 0 && (!workspace || workspace_bytes < need)) return hipErrorInvalidValue;
+    DecodeArgs a{};
+    a.q = p->q;
+    a.k = p->k_pages;
+    a.v = p->v_pages;
+    a.ks = p->k_scale_pages;
+    a.vs = p->v_scale_pages;
+    a.out = p->out;
+    a.lengths = p->lengths;
+    a.k_new = p->k_new;
+    a.v_new = p->v_new;
+    a.pages = page_map(p->block_table, p->page_size, p->max_pages_per_seq, p->num_pages);
+    a.B = p->batch;
+    a.Hq = p->num_q_heads;
+    a.Hkv = p->num_kv_heads;
+    a.G = p->num_q_heads / p->num_kv_heads;
+    a.cap = paged_cap(p);
+    a.d = p->head_dim;
+    a.uniform_len = paged_max_len(p);
+    a.max_len = paged_max_len(p);
+    a.splits = plan.splits;
+    a.chunk = plan.chunk;
+    a.nsg = plan.nsg;
+    const float scale = p->softmax_scale > 0.0f ? p->softmax_scale : 1.0f / sqrtf(static_cast<float>(p->head_dim));
+    a.scale_log2 = scale * kLog2e;
+    bind_workspace(a, plan, workspace);
+    return kvq::launch_decode(a, plan, stream);
+}
+
+hipError_t kvq_paged_append_launch(const kvq_paged_append_params* p, hipStream_t stream) {
+    if (!p || p->batch <= 0 || p->num_kv_heads <= 0 || p->head_dim <= 0 || p->head_dim > KVQ_MAX_HEAD_DIM ||
+        p->page_size <= 0 || p->num_pages <= 0 || p->max_pages_per_seq <= 0 || !p->block_table || !p->k_new ||
+        !p->v_new || !p->k_pages || !p->v_pages || !p->k_scale_pages || !p->v_scale_pages)
+        return hipErrorInvalidValue;
+    const long long cap = static_cast<long long>(p->max_pages_per_seq) * p->page_size;
+    if (cap > INT_MAX || static_cast<long long>(p->batch) * p->num_kv_heads > INT_MAX ||
+        static_cast<long long>(p->batch) * p->max_pages_per_seq > INT_MAX)
+        return hipErrorInvalidValue;
+    return kvq::launch_append(p->k_new, p->v_new, p->k_pages, p->v_pages, p->k_scale_pages, p->v_scale_pages,
+                              p->positions, p->uniform_position, false, p->batch, p->num_kv_heads,
+                              static_cast<int>(cap), static_cast<int>(cap), p->head_dim,
+                              page_map(p->block_table, p->page_size, p->max_pages_per_seq, p->num_pages), stream);
 }
 
 const char* kvq_version(void) { return "kvq 0.1.0 gfx950"; }

@@ -114,7 +114,7 @@ __device__ __forceinline__ void attend(const float (&qr)[SG][16], const int4 (&k
     }
 }
 
-template <int D, int SG>
+template <int D, int SG, bool PAGED>
 __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArgs a) {
     using Geo = FastGeom<D, SG>;
     constexpr int LPT = Geo::LPT;
@@ -186,11 +186,14 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
         for (int j = 0; j < 16; j++) acc[h][j] = 0.0f;
     }
 
+    // Cache row of token t (K/V row at byte row * D, scale at element row).
+    // A wave tile's WSTEP tokens are consecutive rows in either layout: paged
+    // caches run here only when the page size is a multiple of WSTEP.
     const size_t row0 = static_cast<size_t>(bh) * a.cap;
-    const int8_t* kp = a.k + row0 * D + ds * 16;
-    const int8_t* vp = a.v + row0 * D + ds * 16;
-    const float* ksp = a.ks + row0;
-    const float* vsp = a.vs + row0;
+    auto tile_row = [&](int base) -> size_t {
+        if constexpr (PAGED) return cache_row(a.pages, a.Hkv, a.cap, b, kvh, __builtin_amdgcn_readfirstlane(base));
+        else return row0 + base;
+    };
 
     // Main loop.  Lane group tg owns the U consecutive tokens base + tg*U + u,
     // so each 16-byte K/V load instruction still covers whole 128-byte rows
@@ -202,15 +205,20 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
         float ks[U], vs[U];
     };
     auto load_tile = [&](Tile& T, int base) {
+        const size_t r = tile_row(base);  // row of token `base`
+        const int8_t* kp = a.k + r * D + ds * 16;
+        const int8_t* vp = a.v + r * D + ds * 16;
+        const float* ksp = a.ks + r;
+        const float* vsp = a.vs + r;
         const int t_first = base + tg * U;
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int tc = min(t_first + u, tend - 1);
-            T.k[u] = load16_stream(kp + static_cast<size_t>(tc) * D);
-            T.v[u] = load16_stream(vp + static_cast<size_t>(tc) * D);
+            const int tc = min(t_first + u, tend - 1) - base;
+            T.k[u] = load16_stream(kp + static_cast<ptrdiff_t>(tc) * D);
+            T.v[u] = load16_stream(vp + static_cast<ptrdiff_t>(tc) * D);
         }
-        const float* ksu = ksp + t_first;
-        const float* vsu = vsp + t_first;
+        const float* ksu = ksp + (t_first - base);
+        const float* vsu = vsp + (t_first - base);
         const bool vec_ok = ((reinterpret_cast<uintptr_t>(ksu) | reinterpret_cast<uintptr_t>(vsu)) &
                              (sizeof(float) * U - 1)) == 0;
         if (t_first + U <= tend && vec_ok) {
@@ -219,7 +227,7 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
         } else {
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const int tc = min(t_first + u, tend - 1);
+                const int tc = min(t_first + u, tend - 1) - base;
                 T.ks[u] = ksp[tc];
                 T.vs[u] = vsp[tc];
             }
@@ -282,11 +290,12 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
         const float sk1[1] = {sk}, sv1[1] = {sv};
         const int tnew = len - 1;
         if (sgi == 0 && tg == 0) {
-            *reinterpret_cast<int4*>(a.k + (row0 + tnew) * D + ds * 16) = kk1[0];
-            *reinterpret_cast<int4*>(a.v + (row0 + tnew) * D + ds * 16) = vv1[0];
+            const size_t rn = PAGED ? cache_row(a.pages, a.Hkv, a.cap, b, kvh, tnew) : row0 + tnew;
+            *reinterpret_cast<int4*>(a.k + rn * D + ds * 16) = kk1[0];
+            *reinterpret_cast<int4*>(a.v + rn * D + ds * 16) = vv1[0];
             if (ds == 0) {
-                a.ks[row0 + tnew] = sk;
-                a.vs[row0 + tnew] = sv;
+                a.ks[rn] = sk;
+                a.vs[rn] = sv;
             }
         }
         const bool ok1[1] = {tg == 0};
@@ -380,7 +389,6 @@ __global__ __launch_bounds__(kWave) void decode_generic(const DecodeArgs a) {
     if (split >= nsplit) return;
     const int t0 = split * a.chunk;
     const int t1 = min(len, t0 + a.chunk);
-    const size_t row0 = (static_cast<size_t>(b) * a.Hkv + kvh) * a.cap;
 
     for (int i = lane; i < d; i += kWave) {
         qs[i] = a.q[static_cast<size_t>(bhq) * d + i];
@@ -390,17 +398,18 @@ __global__ __launch_bounds__(kWave) void decode_generic(const DecodeArgs a) {
 
     float m = -INFINITY, l = 0.0f;
     for (int t = t0; t < t1; t++) {
-        const int8_t* kr = a.k + (row0 + t) * d;
-        const int8_t* vr = a.v + (row0 + t) * d;
+        const size_t row = cache_row(a.pages, a.Hkv, a.cap, b, kvh, t);
+        const int8_t* kr = a.k + row * d;
+        const int8_t* vr = a.v + row * d;
         float dot = 0.0f;
         for (int i = lane; i < d; i += kWave) dot = fmaf(qs[i], static_cast<float>(kr[i]), dot);
         dot = wave_sum(dot);
-        const float s = (dot * a.ks[row0 + t]) * a.scale_log2;
+        const float s = (dot * a.ks[row]) * a.scale_log2;
         const float mx = fmaxf(m, s);
         const float alpha = fast_exp2(m - mx);
         const float p = fast_exp2(s - mx);
         l = l * alpha + p;
-        const float w = p * a.vs[row0 + t];
+        const float w = p * a.vs[row];
         for (int i = lane; i < d; i += kWave) accs[i] = fmaf(w, static_cast<float>(vr[i]), accs[i] * alpha);
         m = mx;
     }
@@ -416,14 +425,20 @@ __global__ __launch_bounds__(kWave) void decode_generic(const DecodeArgs a) {
     }
 }
 
+template <int D, int SG>
+void launch_fast_sg(const DecodeArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+    if (a.pages.table) hipLaunchKernelGGL((decode_fast<D, SG, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((decode_fast<D, SG, false>), grid, block, 0, stream, a);
+}
+
 template <int D>
 hipError_t launch_fast_d(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(decode_grid(a, p)));
     const dim3 block(kFastWaves * kWave);
     switch (p.sg) {
-        case 1: hipLaunchKernelGGL((decode_fast<D, 1>), grid, block, 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((decode_fast<D, 2>), grid, block, 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((decode_fast<D, 4>), grid, block, 0, stream, a); break;
+        case 1: launch_fast_sg<D, 1>(a, grid, block, stream); break;
+        case 2: launch_fast_sg<D, 2>(a, grid, block, stream); break;
+        case 4: launch_fast_sg<D, 4>(a, grid, block, stream); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -450,6 +465,8 @@ int fast_tile_tokens(int d, int sg) {
         default: return 0;
     }
 }
+
+int fast_wave_tokens(int d, int sg) { return fast_tile_tokens(d, sg) / kFastWaves; }
 
 int fast_heads_per_group(int G) {
     if (G % 4 == 0) return 4;
@@ -497,7 +514,7 @@ hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& p, hipStream_t s
         // Generic path: append first (token length-1 of each sequence), then attend.
         err = launch_append(a.k_new, a.v_new, a.k, a.v, a.ks, a.vs, a.lengths,
                             min(max(a.uniform_len, 0), a.max_len) - 1, true, a.B, a.Hkv, a.max_len,
-                            a.cap, a.d, stream);
+                            a.cap, a.d, a.pages, stream);
         if (err != hipSuccess) return err;
         g.k_new = g.v_new = nullptr;
     }

@@ -79,7 +79,7 @@ __device__ __forceinline__ int pack_bytes(const int* b) {
            static_cast<int>(static_cast<unsigned>(b[3] & 0xff) << 24);
 }
 
-template <int G>
+template <int G, bool PAGED>
 __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma(
     const DecodeArgs a) {
     static_assert(G == 4 || G == 8, "heads per workgroup");
@@ -201,7 +201,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
 
     // This (batch, kv head)'s cache rows as buffer resources: tile loads add a
     // fixed per-lane offset to a wave-uniform tile offset, and a tail tile's
-    // reads past the capacity return 0.
+    // reads past the capacity return 0.  A paged cache gets resources per
+    // tile instead (below).
     const unsigned cap = static_cast<unsigned>(a.cap);
     const buf_rsrc kres = make_rsrc(a.k + row0 * kMD, cap * kMD);
     const buf_rsrc vres = make_rsrc(a.v + row0 * kMD, cap * kMD);
@@ -220,6 +221,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // for later steps (once per kv head).
     float newks = 0.0f, newvs = 0.0f;
     auto append_new = [&]() {
+        const size_t rnew = PAGED ? cache_row(a.pages, a.Hkv, a.cap, b, kvh, tnew) : row0 + tnew;
         newks = quant_scale(wave_max(fmaxf(fabsf(xnew[0]), fabsf(xnew[1]))));
         newvs = quant_scale(wave_max(fmaxf(fabsf(xnew[2]), fabsf(xnew[3]))));
 #pragma unroll
@@ -228,12 +230,12 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         if (sgi == 0) {
             if (lane < 16) {
                 const int row = lane >> 3, piece = lane & 7;
-                *reinterpret_cast<int4*>((row ? a.v : a.k) + (row0 + tnew) * kMD + 16 * piece) =
+                *reinterpret_cast<int4*>((row ? a.v : a.k) + rnew * kMD + 16 * piece) =
                     *reinterpret_cast<const int4*>(&s_newq[row][16 * piece]);
             }
             if (lane == 0) {
-                a.ks[row0 + tnew] = newks;
-                a.vs[row0 + tnew] = newvs;
+                a.ks[rnew] = newks;
+                a.vs[rnew] = newvs;
             }
         }
     };
@@ -255,22 +257,34 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     const int svo = 16 * g;
     auto load_tile = [&](Tile& T, int it) {
         const int base = wbase + it * kMBStep;
-        const int ko = base * kMD;
-        const int so = base * 4;
+        int ko = base * kMD;
+        int so = base * 4;
+        buf_rsrc kr = kres, vr = vres, ksr = ksres, vsr = vsres;
+        if constexpr (PAGED) {
+            // The tile lies in one page (page size a multiple of 32): resources
+            // from its first token to the end of that page.
+            const size_t rp = cache_row(a.pages, a.Hkv, a.cap, b, kvh, base);
+            const unsigned rem = static_cast<unsigned>(a.pages.size - (base & (a.pages.size - 1)));
+            kr = make_rsrc(a.k + rp * kMD, rem * kMD);
+            vr = make_rsrc(a.v + rp * kMD, rem * kMD);
+            ksr = make_rsrc(a.ks + rp, rem * 4u);
+            vsr = make_rsrc(a.vs + rp, rem * 4u);
+            ko = so = 0;
+        }
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            T.ka[s][0] = buffer_load16_stream(kres, kvo + s * 16 * kMD, ko);
-            T.ka[s][1] = buffer_load16_stream(kres, kvo + s * 16 * kMD + 64, ko);
+            T.ka[s][0] = buffer_load16_stream(kr, kvo + s * 16 * kMD, ko);
+            T.ka[s][1] = buffer_load16_stream(kr, kvo + s * 16 * kMD + 64, ko);
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const v4i_t x = buffer_load16_stream(vres, vvo + c * 8 * kMD, ko);
+            const v4i_t x = buffer_load16_stream(vr, vvo + c * 8 * kMD, ko);
             T.v[c] = make_int4(x.x, x.y, x.z, x.w);
         }
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            const v4i_t xk = buffer_load16(ksres, svo + 64 * s, so);
-            const v4i_t xv = buffer_load16(vsres, svo + 64 * s, so);
+            const v4i_t xk = buffer_load16(ksr, svo + 64 * s, so);
+            const v4i_t xv = buffer_load16(vsr, svo + 64 * s, so);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 T.ks[s][i] = __int_as_float(xk[i]);
@@ -484,8 +498,14 @@ hipError_t launch_decode_mfma(const DecodeArgs& a, const DecodePlan& p, hipStrea
     const dim3 grid(static_cast<unsigned>(decode_grid(a, p)));
     const dim3 block(kMWaves * kWave);
     switch (p.sg) {
-        case 4: hipLaunchKernelGGL(decode_mfma<4>, grid, block, 0, stream, a); break;
-        case 8: hipLaunchKernelGGL(decode_mfma<8>, grid, block, 0, stream, a); break;
+        case 4:
+            if (a.pages.table) hipLaunchKernelGGL((decode_mfma<4, true>), grid, block, 0, stream, a);
+            else hipLaunchKernelGGL((decode_mfma<4, false>), grid, block, 0, stream, a);
+            break;
+        case 8:
+            if (a.pages.table) hipLaunchKernelGGL((decode_mfma<8, true>), grid, block, 0, stream, a);
+            else hipLaunchKernelGGL((decode_mfma<8, false>), grid, block, 0, stream, a);
+            break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

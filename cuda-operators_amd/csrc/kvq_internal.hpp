@@ -7,6 +7,25 @@
 
 namespace kvq {
 
+// Paged cache: k/v are page pools [num_pages, Hkv, size, d], their scales
+// [num_pages, Hkv, size]; token t of sequence b is slot t % size of page
+// table[b * max_pages + t / size].  table == null: contiguous layout.
+struct PageMap {
+    const int32_t* table;
+    int size, max_pages, num_pages;
+    int shift;  // log2(size) when size is a power of two, else -1
+};
+
+// Row index of token t of (sequence b, kv head kvh): its K/V row starts at
+// byte row * d, its scale is element row.  Page ids are clamped into
+// [0, num_pages), so a bad table entry cannot address outside the pool.
+__device__ __forceinline__ size_t cache_row(const PageMap& pm, int Hkv, int cap, int b, int kvh, int t) {
+    if (pm.table == nullptr) return (static_cast<size_t>(b) * Hkv + kvh) * cap + t;
+    const int pi = pm.shift >= 0 ? t >> pm.shift : t / pm.size;
+    const int page = min(max(pm.table[static_cast<size_t>(b) * pm.max_pages + pi], 0), pm.num_pages - 1);
+    return (static_cast<size_t>(page) * Hkv + kvh) * pm.size + (t - pi * pm.size);
+}
+
 // Everything one decode launch needs; passed to the kernels by value.
 struct DecodeArgs {
     const float* q;          // [B, Hq, d]
@@ -24,6 +43,7 @@ struct DecodeArgs {
     int* counters;           // [B * Hkv * nsg] arrival counters, or null (merge kernel)
     const int* sched;        // split schedule written by schedule_kernel, or null (static splits)
     int sched_items;         // capacity of the schedule's item list
+    PageMap pages;           // paged layout, or pages.table == null (contiguous rows of cap tokens)
     int B, Hq, Hkv, G, cap, d;
     int uniform_len;         // used when lengths == null
     int max_len;             // every length is clamped to [0, max_len], max_len <= cap
@@ -80,10 +100,11 @@ hipError_t launch_schedule(const int32_t* lengths, int B, int max_len, int units
                            int gran, int items_cap, int* sched, hipStream_t stream);
 // Append one token per (b, kv head).  Position: positions[b] (or uniform_pos
 // when positions is null); with from_lengths, positions holds sequence lengths
-// and the token goes to clamp(lengths[b], 0, max_len) - 1.
+// and the token goes to clamp(lengths[b], 0, max_len) - 1.  Positions outside
+// [0, cap) are skipped (paged: cap = max_pages * page size).
 hipError_t launch_append(const float* k_new, const float* v_new, int8_t* k, int8_t* v, float* ks,
                          float* vs, const int32_t* positions, int uniform_pos, bool from_lengths,
-                         int B, int Hkv, int max_len, int cap, int d, hipStream_t stream);
+                         int B, int Hkv, int max_len, int cap, int d, const PageMap& pages, hipStream_t stream);
 hipError_t launch_quantize_rows(const float* x, int64_t rows, int d, int8_t* q, float* scale,
                                 hipStream_t stream);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
@@ -91,6 +112,8 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 // Tokens one workgroup iteration of the fast kernel covers for head dim d and
 // sg query heads per workgroup; 0 when the fast kernel does not support d.
 int fast_tile_tokens(int d, int sg);
+// Tokens one wave of the fast kernel covers per iteration (its tile).
+int fast_wave_tokens(int d, int sg);
 int fast_heads_per_group(int G);
 // decode_mfma: query heads per workgroup for group size G and head dim d (0:
 // not applicable), tokens per workgroup iteration, launcher.

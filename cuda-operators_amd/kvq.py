@@ -55,8 +55,32 @@ class AppendParams(ctypes.Structure):
     ]
 
 
+class PagedDecodeParams(ctypes.Structure):
+    """struct kvq_paged_decode_params (include/kvq.h)."""
+    _fields_ = [
+        ("batch", _int), ("num_q_heads", _int), ("num_kv_heads", _int), ("head_dim", _int),
+        ("page_size", _int), ("num_pages", _int), ("max_pages_per_seq", _int), ("max_seq_len", _int),
+        ("block_table", _vp), ("lengths", _vp), ("q", _vp), ("k_pages", _vp), ("v_pages", _vp),
+        ("k_scale_pages", _vp), ("v_scale_pages", _vp), ("out", _vp),
+        ("softmax_scale", ctypes.c_float), ("num_splits", _int),
+        ("k_new", _vp), ("v_new", _vp),
+    ]
+
+
+class PagedAppendParams(ctypes.Structure):
+    """struct kvq_paged_append_params (include/kvq.h)."""
+    _fields_ = [
+        ("batch", _int), ("num_kv_heads", _int), ("head_dim", _int), ("page_size", _int),
+        ("num_pages", _int), ("max_pages_per_seq", _int),
+        ("block_table", _vp), ("positions", _vp), ("uniform_position", _int),
+        ("k_new", _vp), ("v_new", _vp), ("k_pages", _vp), ("v_pages", _vp),
+        ("k_scale_pages", _vp), ("v_scale_pages", _vp),
+    ]
+
+
 EXPORTS = ("solve", "kv_int8_split_launch", "kv_int8_simple_launch", "kvq_decode_workspace_size",
            "kvq_workspace_init", "kvq_decode_launch", "kvq_append_launch", "kvq_quantize_rows_launch",
+           "kvq_paged_decode_workspace_size", "kvq_paged_decode_launch", "kvq_paged_append_launch",
            "kvq_version")
 
 
@@ -91,6 +115,12 @@ def lib() -> ctypes.CDLL:
         L.kvq_append_launch.restype = _int
         L.kvq_quantize_rows_launch.argtypes = [_vp, ctypes.c_int64, _int, _vp, _vp, _vp]
         L.kvq_quantize_rows_launch.restype = _int
+        L.kvq_paged_decode_workspace_size.argtypes = [ctypes.POINTER(PagedDecodeParams)]
+        L.kvq_paged_decode_workspace_size.restype = ctypes.c_size_t
+        L.kvq_paged_decode_launch.argtypes = [ctypes.POINTER(PagedDecodeParams), _vp, ctypes.c_size_t, _vp]
+        L.kvq_paged_decode_launch.restype = _int
+        L.kvq_paged_append_launch.argtypes = [ctypes.POINTER(PagedAppendParams), _vp]
+        L.kvq_paged_append_launch.restype = _int
         L.kvq_version.restype = ctypes.c_char_p
         _lib = L
         return L
@@ -249,6 +279,64 @@ def quantize_rows(x, q=None, scale=None, stream=None):
     return q, scale
 
 
+# ---------------------------------------------------------------------------
+# paged cache
+# ---------------------------------------------------------------------------
+class PagedDecoder:
+    """Decode over a paged cache (include/kvq.h part 3) with its own workspace.
+
+    k/v_pages [num_pages, Hkv, page_size, d] int8, k/v_scale_pages
+    [num_pages, Hkv, page_size] fp32, block_table [B, max_pages_per_seq]
+    int32, lengths [B] int32 (required)."""
+
+    def __init__(self, q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, lengths, out,
+                 max_seq_len=0, softmax_scale=0.0, num_splits=0, k_new=None, v_new=None, stream=None):
+        B, Hq, d = q.shape
+        P_, Hkv, page, d2 = k_pages.shape
+        if d2 != d or Hq % Hkv:
+            raise ValueError("shape mismatch")
+        _need(q, torch.float32, (B, Hq, d), "q")
+        for t, n in ((k_pages, "k_pages"), (v_pages, "v_pages")):
+            _need(t, torch.int8, (P_, Hkv, page, d), n)
+        for t, n in ((k_scale_pages, "k_scale_pages"), (v_scale_pages, "v_scale_pages")):
+            _need(t, torch.float32, (P_, Hkv, page), n)
+        if block_table.dim() != 2 or block_table.shape[0] != B:
+            raise ValueError("block_table: want [B, max_pages_per_seq]")
+        _need(block_table, torch.int32, tuple(block_table.shape), "block_table")
+        _need(lengths, torch.int32, (B,), "lengths")
+        _need(out, torch.float32, (B, Hq, d), "out")
+        if k_new is not None:
+            _need(k_new, torch.float32, (B, Hkv, d), "k_new")
+            _need(v_new, torch.float32, (B, Hkv, d), "v_new")
+        self.keep = (q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, lengths, out, k_new, v_new)
+        self.params = PagedDecodeParams(B, Hq, Hkv, d, page, P_, int(block_table.shape[1]), int(max_seq_len),
+                                        _ptr(block_table), _ptr(lengths), _ptr(q), _ptr(k_pages), _ptr(v_pages),
+                                        _ptr(k_scale_pages), _ptr(v_scale_pages), _ptr(out),
+                                        float(softmax_scale), int(num_splits), _ptr(k_new), _ptr(v_new))
+        self.ws_bytes = int(lib().kvq_paged_decode_workspace_size(ctypes.byref(self.params)))
+        self.ws = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=q.device)
+        if self.ws_bytes:
+            workspace_init(self.ws, self.ws_bytes, stream)
+        self._launch = lib().kvq_paged_decode_launch
+        self._args = (ctypes.byref(self.params), _ptr(self.ws), self.ws_bytes)
+
+    def __call__(self, stream=None) -> None:
+        code = self._launch(*self._args, stream if isinstance(stream, int) else _stream(stream))
+        if code != HIP_SUCCESS:
+            raise KvqError("kvq_paged_decode_launch", code)
+
+
+def paged_append(k_new, v_new, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, positions=None,
+                 uniform_position=0, stream=None) -> None:
+    """One new K/V token per (b, kv head) into its page slot (kvq_paged_append_launch)."""
+    P_, Hkv, page, d = k_pages.shape
+    B = block_table.shape[0]
+    p = PagedAppendParams(B, Hkv, d, page, P_, int(block_table.shape[1]), _ptr(block_table), _ptr(positions),
+                          int(uniform_position), _ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages),
+                          _ptr(k_scale_pages), _ptr(v_scale_pages))
+    _check("kvq_paged_append_launch", lib().kvq_paged_append_launch(ctypes.byref(p), _stream(stream)))
+
+
 def default_softmax_scale(d: int) -> float:
     """1/sqrtf(d) in fp32, as kv_cache/KV_int8_split_optimized.cu:335."""
     import numpy as np
@@ -263,4 +351,5 @@ def kv_bytes(lengths, num_kv_heads: int, head_dim: int) -> int:
 
 __all__ = ["lib", "version", "solve", "kv_int8_split_launch", "DecodeParams", "AppendParams", "Decoder",
            "decode", "decode_params", "decode_launch", "workspace_size", "workspace_init", "new_workspace",
-           "append", "quantize_rows", "kv_bytes", "KvqError", "EXPORTS"]
+           "append", "quantize_rows", "kv_bytes", "KvqError", "EXPORTS", "PagedDecodeParams",
+           "PagedAppendParams", "PagedDecoder", "paged_append"]

@@ -91,7 +91,9 @@ typedef struct kvq_decode_params {
     float* v_scale;
     float* out;            /* [B, Hq, d], fully overwritten */
     float softmax_scale;   /* <= 0 selects 1/sqrtf(d) */
-    int num_splits;        /* 0 = choose; otherwise the split count per sequence */
+    int num_splits;        /* 0 = choose; otherwise the split count per sequence (the
+                              tuned kernels round chunks up to whole tiles, so fewer
+                              splits may run) */
     /* Fused append (both NULL = off).  When set, token length_b - 1 of every
      * (b, kv_head) is first quantised from k_new/v_new [B, Hkv, d] fp32 into the
      * cache (int8 values + scale, the same bits as kvq_append_launch), then
@@ -140,6 +142,71 @@ hipError_t kvq_append_launch(const kvq_append_params* p, hipStream_t stream);
  * the same per-row rule as kvq_append_launch. */
 hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, int8_t* q,
                                     float* scale, hipStream_t stream);
+
+/* ============ Part 3: paged KV cache (no counterpart in the reference) ============
+ *
+ * The cache lives in a pool of pages instead of one contiguous row block per
+ * (b, kv_head):
+ *   k/v_pages        [num_pages, Hkv, page_size, d] int8
+ *   k/v_scale_pages  [num_pages, Hkv, page_size]    fp32
+ *   block_table      [batch, max_pages_per_seq]     int32 page ids
+ * Token t of sequence b is slot t % page_size of page
+ * block_table[b * max_pages_per_seq + t / page_size]; within a page each kv
+ * head's page_size rows are contiguous (page_size * d bytes).  Page ids
+ * outside [0, num_pages) are clamped into it on the device (no fault; the
+ * result is then meaningless).  Everything else -- math, lengths, splits,
+ * fused append, workspace rules -- is as for kvq_decode_params, and a paged
+ * cache holding the same tokens gives the same output. */
+
+typedef struct kvq_paged_decode_params {
+    int batch;              /* B >= 1 */
+    int num_q_heads;        /* Hq >= 1, a multiple of num_kv_heads */
+    int num_kv_heads;       /* Hkv >= 1 */
+    int head_dim;           /* d in [1, KVQ_MAX_HEAD_DIM] */
+    int page_size;          /* tokens per page, >= 1 (a multiple of 16 runs the tuned kernels) */
+    int num_pages;          /* pages in the pool, >= 1 */
+    int max_pages_per_seq;  /* row stride of block_table, >= 1 */
+    int max_seq_len;        /* bound on every lengths[b] (0: max_pages_per_seq * page_size) */
+    const int32_t* block_table; /* device [B, max_pages_per_seq] */
+    const int32_t* lengths; /* device [B], required; clamped on device to [0, max_seq_len] */
+    const float* q;         /* [B, Hq, d] */
+    int8_t* k_pages;        /* [num_pages, Hkv, page_size, d]; written only by a fused append */
+    int8_t* v_pages;
+    float* k_scale_pages;   /* [num_pages, Hkv, page_size] */
+    float* v_scale_pages;
+    float* out;             /* [B, Hq, d], fully overwritten */
+    float softmax_scale;    /* <= 0 selects 1/sqrtf(d) */
+    int num_splits;         /* 0 = choose; otherwise the split count per sequence */
+    const float* k_new;     /* fused append as in kvq_decode_params (both NULL = off) */
+    const float* v_new;
+} kvq_paged_decode_params;
+
+/* Workspace bytes for kvq_paged_decode_launch (same rules as
+ * kvq_decode_workspace_size). */
+size_t kvq_paged_decode_workspace_size(const kvq_paged_decode_params* p);
+
+/* Decode attention over a paged cache, plus the optional fused append.
+ * Returns hipErrorInvalidValue before any HIP call on a bad argument or a
+ * workspace smaller than kvq_paged_decode_workspace_size(p). */
+hipError_t kvq_paged_decode_launch(const kvq_paged_decode_params* p, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
+
+typedef struct kvq_paged_append_params {
+    int batch, num_kv_heads, head_dim, page_size, num_pages, max_pages_per_seq;
+    const int32_t* block_table; /* device [B, max_pages_per_seq] */
+    const int32_t* positions;   /* device [B] token position per sequence, or NULL */
+    int uniform_position;       /* used when positions == NULL */
+    const float* k_new;         /* [B, Hkv, d] fp32 */
+    const float* v_new;
+    int8_t* k_pages;            /* [num_pages, Hkv, page_size, d] */
+    int8_t* v_pages;
+    float* k_scale_pages;       /* [num_pages, Hkv, page_size] */
+    float* v_scale_pages;
+} kvq_paged_append_params;
+
+/* kvq_append_launch for a paged cache: the token goes to its position's page
+ * slot; positions outside [0, max_pages_per_seq * page_size) are skipped. */
+hipError_t kvq_paged_append_launch(const kvq_paged_append_params* p, hipStream_t stream);
 
 /* Library version string, e.g. "kvq 0.1.0 gfx950". */
 const char* kvq_version(void);

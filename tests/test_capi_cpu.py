@@ -43,30 +43,35 @@ def test_exports_every_declared_symbol(L):
     assert kvq.version().startswith("kvq ")
 
 
+STRUCTS = {"kvq_decode_params": kvq.DecodeParams, "kvq_append_params": kvq.AppendParams,
+           "kvq_paged_decode_params": kvq.PagedDecodeParams, "kvq_paged_append_params": kvq.PagedAppendParams}
+
+
 def test_struct_layout_matches_c(tmp_path):
     src = tmp_path / "layout.c"
-    fields_d = [f for f, _ in kvq.DecodeParams._fields_]
-    fields_a = [f for f, _ in kvq.AppendParams._fields_]
     lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){"]
-    lines.append('printf("%zu %zu\\n", sizeof(kvq_decode_params), sizeof(kvq_append_params));')
-    for f in fields_d:
-        lines.append(f'printf("d {f} %zu\\n", offsetof(kvq_decode_params, {f}));')
-    for f in fields_a:
-        lines.append(f'printf("a {f} %zu\\n", offsetof(kvq_append_params, {f}));')
+    for cname, cls in STRUCTS.items():
+        lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
     lines.append("return 0;}")
     src.write_text("\n".join(lines))
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c11", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", str(src), "-o", str(exe)],
                    check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
-    sd, sa = map(int, out[0].split())
-    assert sd == ctypes.sizeof(kvq.DecodeParams) and sa == ctypes.sizeof(kvq.AppendParams)
-    for ln in out[1:]:
+    seen = 0
+    for ln in out:
         if not ln:
             continue
-        kind, f, off = ln.split()
-        cls = kvq.DecodeParams if kind == "d" else kvq.AppendParams
-        assert getattr(cls, f).offset == int(off), (kind, f)
+        cname, f, off = ln.split()
+        cls = STRUCTS[cname]
+        if f == "sizeof":
+            assert int(off) == ctypes.sizeof(cls), cname
+        else:
+            assert getattr(cls, f).offset == int(off), (cname, f)
+        seen += 1
+    assert seen == sum(len(c._fields_) + 1 for c in STRUCTS.values())
 
 
 FAKE = 0x1000  # a non-null pointer value that must never be dereferenced
@@ -155,3 +160,46 @@ def test_product_does_not_reference_oracle():
             if f.endswith((".py", ".cpp", ".hip", ".hpp", ".h")):
                 text = open(os.path.join(root, f)).read()
                 assert "oracle" not in text.lower(), f
+
+
+def _paged(**over):
+    p = dict(batch=2, num_q_heads=8, num_kv_heads=2, head_dim=128, page_size=32, num_pages=300,
+             max_pages_per_seq=128, max_seq_len=0, block_table=FAKE, lengths=FAKE, q=FAKE, k_pages=FAKE,
+             v_pages=FAKE, k_scale_pages=FAKE, v_scale_pages=FAKE, out=FAKE, softmax_scale=0.0, num_splits=0,
+             k_new=None, v_new=None)
+    p.update(over)
+    return kvq.PagedDecodeParams(**p)
+
+
+@pytest.mark.parametrize("bad", [dict(batch=0), dict(num_q_heads=7), dict(head_dim=0), dict(head_dim=5000),
+                                 dict(page_size=0), dict(num_pages=0), dict(max_pages_per_seq=0),
+                                 dict(max_seq_len=128 * 32 + 1), dict(block_table=None), dict(lengths=None),
+                                 dict(q=None), dict(k_pages=None), dict(v_scale_pages=None), dict(out=None),
+                                 dict(k_new=FAKE), dict(num_splits=-1), dict(page_size=1 << 20, max_pages_per_seq=4096)],
+                         ids=lambda b: ",".join(f"{k}={v}" for k, v in b.items()))
+def test_paged_decode_rejects_before_hip(L, bad):
+    p = _paged(**bad)
+    assert L.kvq_paged_decode_workspace_size(ctypes.byref(p)) == 0
+    assert L.kvq_paged_decode_launch(ctypes.byref(p), FAKE, 1 << 30, None) == INVALID
+
+
+def test_paged_decode_workspace(L):
+    """Lengths are always device-side, so a paged decode plans the device split
+    schedule: counters + schedule + records for <= B + target/units splits."""
+    p = _paged()
+    need = L.kvq_paged_decode_workspace_size(ctypes.byref(p))
+    assert need > 256 * 1024
+    assert L.kvq_paged_decode_launch(ctypes.byref(p), FAKE, need - 1, None) == INVALID
+    assert L.kvq_paged_decode_workspace_size(ctypes.byref(_paged(num_splits=1))) == 0
+
+
+def test_paged_append_rejects_before_hip(L):
+    ok = dict(batch=2, num_kv_heads=2, head_dim=128, page_size=32, num_pages=10, max_pages_per_seq=4,
+              block_table=FAKE, positions=None, uniform_position=0, k_new=FAKE, v_new=FAKE, k_pages=FAKE,
+              v_pages=FAKE, k_scale_pages=FAKE, v_scale_pages=FAKE)
+    for bad in (dict(block_table=None), dict(k_new=None), dict(page_size=0), dict(num_pages=0),
+                dict(max_pages_per_seq=0), dict(head_dim=0), dict(v_scale_pages=None)):
+        q = dict(ok)
+        q.update(bad)
+        assert L.kvq_paged_append_launch(ctypes.byref(kvq.PagedAppendParams(**q)), None) == INVALID, bad
+    assert L.kvq_paged_append_launch(None, None) == INVALID
