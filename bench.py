@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--config", default="cfg1", help="cfg0..cfg4 (default cfg1, the headline)")
     ap.add_argument("--splits", type=int, default=0, help="splits per sequence (0 = library choice)")
     ap.add_argument("--replicas", type=int, default=0, help="cache replicas (0 = enough for 512 MiB, >= 3)")
+    ap.add_argument("--page-size", type=int, default=0,
+                    help="run the same step through a paged cache with this many tokens per page "
+                         "(pages scattered in a shuffled pool; 0 = contiguous cache)")
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="max seconds for the CPU baseline")
@@ -100,6 +103,40 @@ def cpu_baseline(prob, budget_s):
     }
 
 
+def paged_decoder(kvq, p, out, page, splits, seed):
+    """The problem's cache moved into a pool of `page`-token pages in shuffled
+    order (block table = the shuffle), wrapped in a PagedDecoder."""
+    import torch
+
+    B, Hkv, cap, d = p.k.shape
+    npg = -(-cap // page)
+    gen = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(B * npg, generator=gen).to(p.k.device)
+
+    def pool(x):  # [B, Hkv, cap, ...] -> [B * npg, Hkv, page, ...] in perm order
+        pad = torch.zeros((B, Hkv, npg * page) + tuple(x.shape[3:]), dtype=x.dtype, device=x.device)
+        pad[:, :, :cap] = x
+        pages = pad.view((B, Hkv, npg, page) + tuple(x.shape[3:])).transpose(1, 2)
+        pages = pages.reshape((B * npg, Hkv, page) + tuple(x.shape[3:]))
+        dst = torch.empty(pages.shape, dtype=pages.dtype, device=pages.device)
+        dst[perm] = pages
+        return dst
+
+    table = perm.view(B, npg).to(torch.int32).contiguous()
+    dec = kvq.PagedDecoder(p.q, pool(p.k), pool(p.v), pool(p.ks), pool(p.vs), table, p.lengths, out,
+                           max_seq_len=(0 if p.uniform else p.max_len) or p.cap, num_splits=splits,
+                           k_new=p.k_new, v_new=p.v_new)
+    return dec
+
+
+def kernel_name(base, page):
+    """The tuned kernel the library's planner picks for this problem."""
+    G = base.Hq // base.Hkv
+    mfma = base.d == 128 and G % 4 == 0 and (page == 0 or (page & (page - 1) == 0 and page % 32 == 0))
+    name = "decode_mfma" if mfma else "decode_fast"
+    return name + (" (+ schedule_kernel per step)" if not base.uniform else "")
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -128,10 +165,14 @@ def main():
                           base.lengths, base.k_new, base.v_new)
         reps.append(c)
     outs = [torch.empty_like(base.q) for _ in reps]
-    decs = [kvq.Decoder(p.q, p.k, p.v, p.ks, p.vs, o, lengths=p.lengths,
-                        max_seq_len=(0 if p.uniform else p.max_len) or p.cap,
-                        num_splits=args.splits, k_new=p.k_new, v_new=p.v_new)
-            for p, o in zip(reps, outs)]
+    if args.page_size > 0:
+        decs = [paged_decoder(kvq, p, o, args.page_size, args.splits, args.seed + i)
+                for i, (p, o) in enumerate(zip(reps, outs))]
+    else:
+        decs = [kvq.Decoder(p.q, p.k, p.v, p.ks, p.vs, o, lengths=p.lengths,
+                            max_seq_len=(0 if p.uniform else p.max_len) or p.cap,
+                            num_splits=args.splits, k_new=p.k_new, v_new=p.v_new)
+                for p, o in zip(reps, outs)]
     torch.cuda.synchronize()
 
     # Launches go to the current stream by its raw handle: one foreign call
@@ -190,7 +231,7 @@ def main():
         del x, y
 
     gbps = kv_bytes / (ms_per_step * 1e-3) / 1e9
-    achieved = gbps  # one decode_fast launch per step
+    achieved = gbps  # the step's decode launch(es)
     traffic = None
     if os.path.exists(args.traffic):
         try:
@@ -225,11 +266,12 @@ def main():
             "kv_bytes_per_step": kv_bytes,
             "replicas": R,
             "splits": decs[0].params.num_splits or "auto",
+            "layout": f"paged, {args.page_size} tokens per page" if args.page_size > 0 else "contiguous",
             "parallelism": "single GPU",
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_fast",
+            "kernel": kernel_name(base, args.page_size),
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

@@ -271,8 +271,9 @@ bool paged_params_ok(const kvq_paged_decode_params* p) {
     if (p->page_size <= 0 || p->num_pages <= 0 || p->max_pages_per_seq <= 0) return false;
     const long long cap = static_cast<long long>(p->max_pages_per_seq) * p->page_size;
     if (cap > INT_MAX || p->max_seq_len < 0 || p->max_seq_len > cap || p->num_splits < 0) return false;
-    if (!p->block_table || !p->lengths || !p->q || !p->k_pages || !p->v_pages || !p->k_scale_pages ||
-        !p->v_scale_pages || !p->out)
+    if (!p->lengths && p->max_seq_len == 0) return false;
+    if (!p->block_table || !p->q || !p->k_pages || !p->v_pages || !p->k_scale_pages || !p->v_scale_pages ||
+        !p->out)
         return false;
     if ((p->k_new == nullptr) != (p->v_new == nullptr)) return false;
     if (static_cast<long long>(p->batch) * p->num_q_heads > INT_MAX / 4) return false;
@@ -296,7 +297,7 @@ DecodePlan paged_plan(const kvq_paged_decode_params* p) {
                          (p->head_dim % 16) == 0 && (!p->k_new || (aligned16(p->k_new) && aligned16(p->v_new)));
     const bool quads = aligned16(p->k_scale_pages) && aligned16(p->v_scale_pages);
     return make_plan(p->batch, p->num_q_heads, p->num_kv_heads, p->head_dim, paged_max_len(p), aligned, quads,
-                     p->page_size, true, p->num_splits, INT_MAX, true);
+                     p->page_size, p->lengths != nullptr, p->num_splits, INT_MAX, true);
 }
 
 }  // namespace

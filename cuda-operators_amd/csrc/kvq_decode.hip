@@ -186,14 +186,10 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
         for (int j = 0; j < 16; j++) acc[h][j] = 0.0f;
     }
 
-    // Cache row of token t (K/V row at byte row * D, scale at element row).
-    // A wave tile's WSTEP tokens are consecutive rows in either layout: paged
-    // caches run here only when the page size is a multiple of WSTEP.
+    // Cache rows (K/V row at byte row * D, scale at element row).  A wave
+    // tile's WSTEP tokens are consecutive rows in either layout: paged caches
+    // run here only with power-of-two pages that are a multiple of WSTEP.
     const size_t row0 = static_cast<size_t>(bh) * a.cap;
-    auto tile_row = [&](int base) -> size_t {
-        if constexpr (PAGED) return cache_row(a.pages, a.Hkv, a.cap, b, kvh, __builtin_amdgcn_readfirstlane(base));
-        else return row0 + base;
-    };
 
     // Main loop.  Lane group tg owns the U consecutive tokens base + tg*U + u,
     // so each 16-byte K/V load instruction still covers whole 128-byte rows
@@ -204,8 +200,7 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
         int4 k[U], v[U];
         float ks[U], vs[U];
     };
-    auto load_tile = [&](Tile& T, int base) {
-        const size_t r = tile_row(base);  // row of token `base`
+    auto load_tile = [&](Tile& T, int base, size_t r) {  // r: row of token `base`
         const int8_t* kp = a.k + r * D + ds * 16;
         const int8_t* vp = a.v + r * D + ds * 16;
         const float* ksp = a.ks + r;
@@ -239,24 +234,45 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
         for (int u = 0; u < U; u++) ok[u] = base + tg * U + u < tend;
         attend<SG, U, LPT>(qr, T.k, T.v, T.ks, T.vs, ok, a.scale_log2, m, l, acc);
     };
-    int base = t0 + wave * Geo::WSTEP;
+    int base = t0 + __builtin_amdgcn_readfirstlane(wave) * Geo::WSTEP;  // wave-uniform
+    // In a paged cache (power-of-two pages here) the next tile's block-table
+    // entry is fetched one tile ahead and only turned into a row when that tile
+    // loads, so the scalar load's latency stays off the load path.  The index is
+    // clamped to this sequence's last token: the table is never read past the
+    // sequence's own entries.
+    auto page_entry = [&](int t) -> int {
+        if constexpr (PAGED)
+            return a.pages.table[static_cast<size_t>(b) * a.pages.max_pages + (min(t, tend - 1) >> a.pages.shift)];
+        else return 0;
+    };
+    int pg_next = page_entry(base);
+    auto next_row = [&](int nb) -> size_t {  // row of the tile at nb - BSTEP; prefetch nb's entry
+        const int tb = nb - Geo::BSTEP;
+        if constexpr (PAGED) {
+            const int page = min(max(pg_next, 0), a.pages.num_pages - 1);
+            pg_next = page_entry(nb);
+            return (static_cast<size_t>(page) * a.Hkv + kvh) * a.pages.size + (tb & (a.pages.size - 1));
+        } else {
+            return row0 + tb;
+        }
+    };
     if constexpr (!Geo::PIPE) {
         for (; base < tend; base += Geo::BSTEP) {
             Tile tt;
-            load_tile(tt, base);
+            load_tile(tt, base, next_row(base + Geo::BSTEP));
             run_tile(tt, base);
         }
     } else {
         Tile ta, tb;
-        if (base < tend) load_tile(ta, base);
+        if (base < tend) load_tile(ta, base, next_row(base + Geo::BSTEP));
         while (base < tend) {
             int nb = base + Geo::BSTEP;
-            if (nb < tend) load_tile(tb, nb);
+            if (nb < tend) load_tile(tb, nb, next_row(nb + Geo::BSTEP));
             run_tile(ta, base);
             base = nb;
             if (base >= tend) break;
             nb = base + Geo::BSTEP;
-            if (nb < tend) load_tile(ta, nb);
+            if (nb < tend) load_tile(ta, nb, next_row(nb + Geo::BSTEP));
             run_tile(tb, base);
             base = nb;
         }

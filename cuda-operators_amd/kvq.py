@@ -287,7 +287,7 @@ class PagedDecoder:
 
     k/v_pages [num_pages, Hkv, page_size, d] int8, k/v_scale_pages
     [num_pages, Hkv, page_size] fp32, block_table [B, max_pages_per_seq]
-    int32, lengths [B] int32 (required)."""
+    int32, lengths [B] int32 (or None with a uniform max_seq_len)."""
 
     def __init__(self, q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, lengths, out,
                  max_seq_len=0, softmax_scale=0.0, num_splits=0, k_new=None, v_new=None, stream=None):
@@ -303,7 +303,8 @@ class PagedDecoder:
         if block_table.dim() != 2 or block_table.shape[0] != B:
             raise ValueError("block_table: want [B, max_pages_per_seq]")
         _need(block_table, torch.int32, tuple(block_table.shape), "block_table")
-        _need(lengths, torch.int32, (B,), "lengths")
+        if lengths is not None:
+            _need(lengths, torch.int32, (B,), "lengths")
         _need(out, torch.float32, (B, Hq, d), "out")
         if k_new is not None:
             _need(k_new, torch.float32, (B, Hkv, d), "k_new")

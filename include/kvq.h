@@ -166,9 +166,10 @@ typedef struct kvq_paged_decode_params {
     int page_size;          /* tokens per page, >= 1 (a multiple of 16 runs the tuned kernels) */
     int num_pages;          /* pages in the pool, >= 1 */
     int max_pages_per_seq;  /* row stride of block_table, >= 1 */
-    int max_seq_len;        /* bound on every lengths[b] (0: max_pages_per_seq * page_size) */
+    int max_seq_len;        /* uniform length when lengths == NULL; otherwise a bound on
+                               every lengths[b] (0: max_pages_per_seq * page_size) */
     const int32_t* block_table; /* device [B, max_pages_per_seq] */
-    const int32_t* lengths; /* device [B], required; clamped on device to [0, max_seq_len] */
+    const int32_t* lengths; /* device [B] or NULL; clamped on device to [0, max_seq_len] */
     const float* q;         /* [B, Hq, d] */
     int8_t* k_pages;        /* [num_pages, Hkv, page_size, d]; written only by a fused append */
     int8_t* v_pages;

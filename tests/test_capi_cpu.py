@@ -173,7 +173,8 @@ def _paged(**over):
 
 @pytest.mark.parametrize("bad", [dict(batch=0), dict(num_q_heads=7), dict(head_dim=0), dict(head_dim=5000),
                                  dict(page_size=0), dict(num_pages=0), dict(max_pages_per_seq=0),
-                                 dict(max_seq_len=128 * 32 + 1), dict(block_table=None), dict(lengths=None),
+                                 dict(max_seq_len=128 * 32 + 1), dict(block_table=None),
+                                 dict(lengths=None, max_seq_len=0),
                                  dict(q=None), dict(k_pages=None), dict(v_scale_pages=None), dict(out=None),
                                  dict(k_new=FAKE), dict(num_splits=-1), dict(page_size=1 << 20, max_pages_per_seq=4096)],
                          ids=lambda b: ",".join(f"{k}={v}" for k, v in b.items()))

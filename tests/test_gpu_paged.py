@@ -196,3 +196,22 @@ def test_paged_repeated_launches(o):
         torch.cuda.synchronize()
         want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
         assert_close(down(out), want, what=f"paged launch {it}")
+
+
+@pytest.mark.parametrize("G,page", [(1, 32), (8, 64)])
+def test_paged_uniform_length(o, G, page):
+    """lengths == NULL: every sequence has max_seq_len tokens (static splits,
+    no schedule launch); bitwise equal to the contiguous uniform decode, with
+    the fused append."""
+    rng = np.random.default_rng(40 + G + page)
+    B, Hkv, cap, d, L = 3, 2, 512, 128, 448
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows)
+    kn = rng.standard_normal((B, Hkv, d)).astype(np.float32)
+    vn = rng.standard_normal((B, Hkv, d)).astype(np.float32)
+    kp, vp, ksp, vsp, table = to_pages(rng, p["k"], p["v"], p["ks"], p["vs"], np.full(B, cap), page)
+    g = [up(x) for x in (p["q"], kp, vp, ksp, vsp, table, kn, vn)]
+    out = _gpu.poisoned(p["q"].shape)
+    kvq.PagedDecoder(g[0], g[1], g[2], g[3], g[4], g[5], None, out, max_seq_len=L, k_new=g[6], v_new=g[7])()
+    torch.cuda.synchronize()
+    ref = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], max_seq_len=L, k_new=kn, v_new=vn)[0]
+    assert np.array_equal(_bits(down(out)), _bits(ref))
