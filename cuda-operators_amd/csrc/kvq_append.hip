@@ -52,6 +52,124 @@ __global__ __launch_bounds__(kQuantWaves* kWave) void quantize_rows_kernel(const
         quantize_row_wave(x + r * d, d, q + r * d, scale + r, lane);
 }
 
+// ---------------------------------------------------------------------------
+// Prefill quantiser: L new K and V rows per (b, kv head) into the cache.
+// ---------------------------------------------------------------------------
+
+// Element e of an input row as fp32 (bf16 is widened exactly).
+template <bool BF16>
+__device__ __forceinline__ float load_elem(const void* row, int e) {
+    if constexpr (BF16) return __uint_as_float(static_cast<unsigned>(static_cast<const uint16_t*>(row)[e]) << 16);
+    else return static_cast<const float*>(row)[e];
+}
+
+// Max over aligned groups of N lanes (N a power of two <= 64).
+template <int N>
+__device__ __forceinline__ float lanes_max(float x) {
+    if constexpr (N <= 16) {
+        return group_max<N>(x);
+    } else {
+        x = group_max<16>(x);
+        x = fmaxf(x, __shfl_xor(x, 16));
+        if constexpr (N == 64) x = fmaxf(x, __shfl_xor(x, 32));
+        return x;
+    }
+}
+
+// Tuned path: LPR lanes read one row with a 16-byte load each (fp32: 4
+// elements, bf16: 8), so one wave load covers 64 / LPR whole rows; kPrefillU
+// wave loads are in flight per lane.  Each lane packs its quantised elements
+// into one 4- or 8-byte store, so a row's int8 bytes go out contiguous.
+constexpr int kPrefillWaves = 4;
+constexpr int kPrefillU = 4;
+
+template <int D, bool BF16>
+__global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const PrefillArgs a) {
+    constexpr int EPL = BF16 ? 8 : 4;
+    constexpr int LPR = D / EPL;
+    constexpr int RPW = kWave / LPR;
+    static_assert(LPR >= 1 && LPR <= kWave && (kWave % LPR) == 0, "row geometry");
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int slot = lane / LPR;  // row within a wave load
+    const int ls = lane % LPR;    // 16-byte piece of the row
+    const int kv = blockIdx.y;    // 0: K rows, 1: V rows
+    const char* x = static_cast<const char*>(kv ? a.v_new : a.k_new);
+    int8_t* qo = kv ? a.v : a.k;
+    float* so = kv ? a.vs : a.ks;
+    constexpr int ESZ = BF16 ? 2 : 4;
+    const unsigned step = gridDim.x * kPrefillWaves * RPW * kPrefillU;
+    for (unsigned r0 = (blockIdx.x * kPrefillWaves + wave) * RPW * kPrefillU; r0 < a.rows; r0 += step) {
+        int4 raw[kPrefillU];
+#pragma unroll
+        for (int u = 0; u < kPrefillU; u++) {
+            const unsigned row = r0 + u * RPW + slot;
+            raw[u] = row < a.rows ? *reinterpret_cast<const int4*>(x + (static_cast<size_t>(row) * D + ls * EPL) * ESZ)
+                                  : make_int4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < kPrefillU; u++) {
+            const unsigned row = r0 + u * RPW + slot;
+            float e[EPL];
+            const int w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+            for (int i = 0; i < EPL; i++) {
+                if constexpr (BF16) e[i] = __uint_as_float((i & 1) ? (static_cast<unsigned>(w[i >> 1]) & 0xffff0000u)
+                                                                 : (static_cast<unsigned>(w[i >> 1]) << 16));
+                else e[i] = __int_as_float(w[i]);
+            }
+            float am = 0.0f;
+#pragma unroll
+            for (int i = 0; i < EPL; i++) am = fmaxf(am, fabsf(e[i]));
+            const float scale = quant_scale(lanes_max<LPR>(am));
+            if (row >= a.rows) continue;
+            const unsigned bh = row / a.L;
+            const int t = static_cast<int>(row - bh * a.L);
+            const int b = static_cast<int>(bh / a.Hkv);
+            const int h = static_cast<int>(bh - static_cast<unsigned>(b) * a.Hkv);
+            const int pos = (a.start ? a.start[b] : a.uniform_start) + t;
+            if (pos < 0 || pos >= a.cap) continue;
+            const size_t orow = cache_row(a.pages, a.Hkv, a.cap, b, h, pos);
+            int qv[EPL];
+#pragma unroll
+            for (int i = 0; i < EPL; i++) qv[i] = quant_one(e[i], scale);
+            if constexpr (BF16) {
+                const int2 pk = make_int2(pack4(qv[0], qv[1], qv[2], qv[3]), pack4(qv[4], qv[5], qv[6], qv[7]));
+                *reinterpret_cast<int2*>(qo + orow * D + ls * EPL) = pk;
+            } else {
+                *reinterpret_cast<int*>(qo + orow * D + ls * EPL) = pack4(qv[0], qv[1], qv[2], qv[3]);
+            }
+            if (ls == 0) so[orow] = scale;
+        }
+    }
+}
+
+// Any head dim / alignment: one wave per row, lanes striding over it.
+template <bool BF16>
+__global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_generic_kernel(const PrefillArgs a, int d) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int kv = blockIdx.y;
+    const char* x = static_cast<const char*>(kv ? a.v_new : a.k_new);
+    int8_t* qo = kv ? a.v : a.k;
+    float* so = kv ? a.vs : a.ks;
+    const unsigned step = gridDim.x * kPrefillWaves;
+    for (unsigned row = blockIdx.x * kPrefillWaves + threadIdx.x / kWave; row < a.rows; row += step) {
+        const void* xr = x + static_cast<size_t>(row) * d * (BF16 ? 2 : 4);
+        const unsigned bh = row / a.L;
+        const int t = static_cast<int>(row - bh * a.L);
+        const int b = static_cast<int>(bh / a.Hkv);
+        const int h = static_cast<int>(bh - static_cast<unsigned>(b) * a.Hkv);
+        const int pos = (a.start ? a.start[b] : a.uniform_start) + t;
+        if (pos < 0 || pos >= a.cap) continue;
+        const size_t orow = cache_row(a.pages, a.Hkv, a.cap, b, h, pos);
+        float am = 0.0f;
+        for (int i = lane; i < d; i += kWave) am = fmaxf(am, fabsf(load_elem<BF16>(xr, i)));
+        const float scale = quant_scale(wave_max(am));
+        for (int i = lane; i < d; i += kWave) qo[orow * d + i] = static_cast<int8_t>(quant_one(load_elem<BF16>(xr, i), scale));
+        if (lane == 0) so[orow] = scale;
+    }
+}
+
 __global__ __launch_bounds__(256) void fill_zero_kernel(uint8_t* p, size_t bytes) {
     const size_t words = bytes / 4;
     uint32_t* w = reinterpret_cast<uint32_t*>(p);
@@ -80,6 +198,40 @@ hipError_t launch_quantize_rows(const float* x, int64_t rows, int d, int8_t* q, 
     hipLaunchKernelGGL(quantize_rows_kernel, dim3(grid), dim3(kQuantWaves * kWave), 0, stream, x, rows,
                        d, q, scale);
     return hipGetLastError();
+}
+
+template <bool BF16>
+hipError_t launch_prefill_t(const PrefillArgs& a, int d, bool vec_ok, hipStream_t stream) {
+    const unsigned want_rows = static_cast<unsigned>(a.rows);
+    auto grid_for = [&](unsigned rows_per_wg) {
+        const unsigned wgs = (want_rows + rows_per_wg - 1) / rows_per_wg;
+        return dim3(wgs < 8192 ? (wgs ? wgs : 1) : 8192, static_cast<unsigned>(a.planes));
+    };
+    const dim3 block(kPrefillWaves * kWave);
+    constexpr int EPL = BF16 ? 8 : 4;
+    if (vec_ok) {
+        switch (d) {
+#define KVQ_PREFILL_CASE(DD)                                                                        \
+    case DD:                                                                                        \
+        hipLaunchKernelGGL((prefill_kernel<DD, BF16>),                                              \
+                           grid_for(kPrefillWaves * (kWave / (DD / EPL)) * kPrefillU), block, 0,    \
+                           stream, a);                                                              \
+        return hipGetLastError();
+            KVQ_PREFILL_CASE(32)
+            KVQ_PREFILL_CASE(64)
+            KVQ_PREFILL_CASE(128)
+            KVQ_PREFILL_CASE(256)
+#undef KVQ_PREFILL_CASE
+            default: break;
+        }
+    }
+    hipLaunchKernelGGL((prefill_generic_kernel<BF16>), grid_for(kPrefillWaves), block, 0, stream, a, d);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill(const PrefillArgs& a, int d, bool bf16, bool vec_ok, hipStream_t stream) {
+    if (a.rows == 0) return hipSuccess;
+    return bf16 ? launch_prefill_t<true>(a, d, vec_ok, stream) : launch_prefill_t<false>(a, d, vec_ok, stream);
 }
 
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream) {

@@ -402,6 +402,21 @@ hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, 
                                     hipStream_t stream) {
     if (rows < 0 || head_dim <= 0 || head_dim > KVQ_MAX_HEAD_DIM) return hipErrorInvalidValue;
     if (rows > 0 && (!x || !q || !scale)) return hipErrorInvalidValue;
+    const bool tuned_d = head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256;
+    if (rows > 0 && rows < (1LL << 31) && tuned_d && aligned16(x) && (reinterpret_cast<uintptr_t>(q) & 7u) == 0) {
+        // The prefill kernel over one plane of `rows` tokens at positions 0..rows-1.
+        kvq::PrefillArgs a{};
+        a.k_new = a.v_new = x;
+        a.k = a.v = q;
+        a.ks = a.vs = scale;
+        a.Hkv = 1;
+        a.L = static_cast<int>(rows);
+        a.cap = static_cast<int>(rows);
+        a.rows = static_cast<unsigned>(rows);
+        a.planes = 1;
+        a.pages = kvq::PageMap{nullptr, 0, 0, 0, -1};
+        return kvq::launch_prefill(a, head_dim, false, true, stream);
+    }
     return kvq::launch_quantize_rows(x, rows, head_dim, q, scale, stream);
 }
 
@@ -457,6 +472,44 @@ hipError_t kvq_paged_append_launch(const kvq_paged_append_params* p, hipStream_t
                               p->positions, p->uniform_position, false, p->batch, p->num_kv_heads,
                               static_cast<int>(cap), static_cast<int>(cap), p->head_dim,
                               page_map(p->block_table, p->page_size, p->max_pages_per_seq, p->num_pages), stream);
+}
+
+hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t stream) {
+    if (!p || p->batch <= 0 || p->num_kv_heads <= 0 || p->head_dim <= 0 || p->head_dim > KVQ_MAX_HEAD_DIM ||
+        p->tokens < 0 || (p->dtype != KVQ_DTYPE_F32 && p->dtype != KVQ_DTYPE_BF16))
+        return hipErrorInvalidValue;
+    if (!p->k_new || !p->v_new || !p->k_cache || !p->v_cache || !p->k_scale || !p->v_scale)
+        return hipErrorInvalidValue;
+    const long long rows = static_cast<long long>(p->batch) * p->num_kv_heads * p->tokens;
+    if (rows >= (1LL << 31)) return hipErrorInvalidValue;
+    kvq::PrefillArgs a{};
+    if (p->block_table) {
+        if (p->page_size <= 0 || p->num_pages <= 0 || p->max_pages_per_seq <= 0) return hipErrorInvalidValue;
+        const long long cap = static_cast<long long>(p->max_pages_per_seq) * p->page_size;
+        if (cap > INT_MAX || static_cast<long long>(p->batch) * p->max_pages_per_seq > INT_MAX)
+            return hipErrorInvalidValue;
+        a.cap = static_cast<int>(cap);
+        a.pages = page_map(p->block_table, p->page_size, p->max_pages_per_seq, p->num_pages);
+    } else {
+        if (p->capacity <= 0) return hipErrorInvalidValue;
+        a.cap = p->capacity;
+        a.pages = kvq::PageMap{nullptr, 0, 0, 0, -1};
+    }
+    a.k_new = p->k_new;
+    a.v_new = p->v_new;
+    a.k = p->k_cache;
+    a.v = p->v_cache;
+    a.ks = p->k_scale;
+    a.vs = p->v_scale;
+    a.start = p->start;
+    a.uniform_start = p->uniform_start;
+    a.Hkv = p->num_kv_heads;
+    a.L = p->tokens;
+    a.rows = static_cast<unsigned>(rows);
+    a.planes = 2;
+    const bool vec_ok = aligned16(p->k_new) && aligned16(p->v_new) &&
+                        ((reinterpret_cast<uintptr_t>(p->k_cache) | reinterpret_cast<uintptr_t>(p->v_cache)) & 7u) == 0;
+    return kvq::launch_prefill(a, p->head_dim, p->dtype == KVQ_DTYPE_BF16, vec_ok, stream);
 }
 
 const char* kvq_version(void) { return "kvq 0.1.0 gfx950"; }

@@ -107,6 +107,27 @@ hipError_t launch_append(const float* k_new, const float* v_new, int8_t* k, int8
                          int B, int Hkv, int max_len, int cap, int d, const PageMap& pages, hipStream_t stream);
 hipError_t launch_quantize_rows(const float* x, int64_t rows, int d, int8_t* q, float* scale,
                                 hipStream_t stream);
+
+// Prefill: rows = B * Hkv * L input rows of K and of V ([B, Hkv, L, d], fp32
+// or bf16), row (b, h, t) to cache position start_b + t (skipped outside
+// [0, cap)).
+struct PrefillArgs {
+    const void* k_new;
+    const void* v_new;
+    int8_t* k;
+    int8_t* v;
+    float* ks;
+    float* vs;
+    const int32_t* start;
+    int uniform_start;
+    int Hkv, L, cap;
+    unsigned rows;
+    int planes;  // 2: K and V; 1: K only
+    PageMap pages;
+};
+// vec_ok: 16-byte aligned inputs and 8-byte aligned caches (tuned kernel for
+// d in {32, 64, 128, 256}).
+hipError_t launch_prefill(const PrefillArgs& a, int d, bool bf16, bool vec_ok, hipStream_t stream);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 
 // Tokens one workgroup iteration of the fast kernel covers for head dim d and

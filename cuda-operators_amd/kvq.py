@@ -78,10 +78,23 @@ class PagedAppendParams(ctypes.Structure):
     ]
 
 
+class PrefillParams(ctypes.Structure):
+    """struct kvq_prefill_params (include/kvq.h)."""
+    _fields_ = [
+        ("batch", _int), ("num_kv_heads", _int), ("head_dim", _int), ("tokens", _int), ("dtype", _int),
+        ("k_new", _vp), ("v_new", _vp), ("start", _vp), ("uniform_start", _int), ("capacity", _int),
+        ("k_cache", _vp), ("v_cache", _vp), ("k_scale", _vp), ("v_scale", _vp),
+        ("block_table", _vp), ("page_size", _int), ("num_pages", _int), ("max_pages_per_seq", _int),
+    ]
+
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
 EXPORTS = ("solve", "kv_int8_split_launch", "kv_int8_simple_launch", "kvq_decode_workspace_size",
            "kvq_workspace_init", "kvq_decode_launch", "kvq_append_launch", "kvq_quantize_rows_launch",
            "kvq_paged_decode_workspace_size", "kvq_paged_decode_launch", "kvq_paged_append_launch",
-           "kvq_version")
+           "kvq_prefill_quantize_launch", "kvq_version")
 
 
 class KvqError(RuntimeError):
@@ -121,6 +134,8 @@ def lib() -> ctypes.CDLL:
         L.kvq_paged_decode_launch.restype = _int
         L.kvq_paged_append_launch.argtypes = [ctypes.POINTER(PagedAppendParams), _vp]
         L.kvq_paged_append_launch.restype = _int
+        L.kvq_prefill_quantize_launch.argtypes = [ctypes.POINTER(PrefillParams), _vp]
+        L.kvq_prefill_quantize_launch.restype = _int
         L.kvq_version.restype = ctypes.c_char_p
         _lib = L
         return L
@@ -338,6 +353,33 @@ def paged_append(k_new, v_new, k_pages, v_pages, k_scale_pages, v_scale_pages, b
     _check("kvq_paged_append_launch", lib().kvq_paged_append_launch(ctypes.byref(p), _stream(stream)))
 
 
+def prefill(k_new, v_new, k_cache, v_cache, k_scale, v_scale, start=None, uniform_start=0, block_table=None,
+            stream=None) -> None:
+    """Quantise L new tokens per (b, kv head) into the cache (kvq_prefill_quantize_launch).
+
+    k_new/v_new [B, Hkv, L, d] fp32 or bf16; the cache is contiguous
+    ([B, Hkv, cap, d]) or, with block_table [B, max_pages], a page pool
+    ([num_pages, Hkv, page_size, d]); start [B] int32 or uniform_start."""
+    B, Hkv, L, d = k_new.shape
+    if k_new.dtype == torch.bfloat16:
+        dt = DTYPE_BF16
+    elif k_new.dtype == torch.float32:
+        dt = DTYPE_F32
+    else:
+        raise TypeError("k_new must be float32 or bfloat16")
+    for t, n in ((k_new, "k_new"), (v_new, "v_new")):
+        _need(t, k_new.dtype, (B, Hkv, L, d), n)
+    if block_table is None:
+        cap = k_cache.shape[2]
+        pg = (0, 0, 0)
+    else:
+        cap = 0
+        pg = (k_cache.shape[2], k_cache.shape[0], int(block_table.shape[1]))
+    p = PrefillParams(B, Hkv, d, L, dt, _ptr(k_new), _ptr(v_new), _ptr(start), int(uniform_start), cap,
+                      _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_table), *pg)
+    _check("kvq_prefill_quantize_launch", lib().kvq_prefill_quantize_launch(ctypes.byref(p), _stream(stream)))
+
+
 def default_softmax_scale(d: int) -> float:
     """1/sqrtf(d) in fp32, as kv_cache/KV_int8_split_optimized.cu:335."""
     import numpy as np
@@ -353,4 +395,5 @@ def kv_bytes(lengths, num_kv_heads: int, head_dim: int) -> int:
 __all__ = ["lib", "version", "solve", "kv_int8_split_launch", "DecodeParams", "AppendParams", "Decoder",
            "decode", "decode_params", "decode_launch", "workspace_size", "workspace_init", "new_workspace",
            "append", "quantize_rows", "kv_bytes", "KvqError", "EXPORTS", "PagedDecodeParams",
-           "PagedAppendParams", "PagedDecoder", "paged_append"]
+           "PagedAppendParams", "PagedDecoder", "paged_append", "PrefillParams", "prefill", "DTYPE_F32",
+           "DTYPE_BF16"]

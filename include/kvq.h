@@ -209,6 +209,38 @@ typedef struct kvq_paged_append_params {
  * slot; positions outside [0, max_pages_per_seq * page_size) are skipped. */
 hipError_t kvq_paged_append_launch(const kvq_paged_append_params* p, hipStream_t stream);
 
+/* ============ Part 4: prefill quantiser (no counterpart in the reference) ============
+ *
+ * Writes L new tokens per (b, kv head) into a contiguous or paged cache:
+ * K and V rows x[B, Hkv, L, d] (fp32 or bf16) are quantised with the rule of
+ * kvq_append_launch and stored at token positions start_b .. start_b + L - 1
+ * (start_b = start[b], or uniform_start when start is NULL).  Positions
+ * outside [0, capacity) -- paged: [0, max_pages_per_seq * page_size) -- are
+ * skipped.  bf16 inputs are widened to fp32 exactly before the same rule. */
+
+#define KVQ_DTYPE_F32 0
+#define KVQ_DTYPE_BF16 1
+
+typedef struct kvq_prefill_params {
+    int batch, num_kv_heads, head_dim;
+    int tokens;               /* L >= 0 new tokens per (b, kv head) */
+    int dtype;                /* KVQ_DTYPE_F32 or KVQ_DTYPE_BF16 */
+    const void* k_new;        /* [B, Hkv, L, d] */
+    const void* v_new;
+    const int32_t* start;     /* device [B] first position per sequence, or NULL */
+    int uniform_start;        /* used when start == NULL */
+    int capacity;             /* contiguous cache: tokens per (b, kv head) row block */
+    int8_t* k_cache;          /* contiguous [B, Hkv, capacity, d] or pages [num_pages, Hkv, page_size, d] */
+    int8_t* v_cache;
+    float* k_scale;           /* [B, Hkv, capacity] or [num_pages, Hkv, page_size] */
+    float* v_scale;
+    const int32_t* block_table; /* NULL: contiguous cache; else paged (as kvq_paged_decode_params) */
+    int page_size, num_pages, max_pages_per_seq;
+} kvq_prefill_params;
+
+/* One launch quantises all B*Hkv*L K and V rows. */
+hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t stream);
+
 /* Library version string, e.g. "kvq 0.1.0 gfx950". */
 const char* kvq_version(void);
 

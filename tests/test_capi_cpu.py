@@ -44,7 +44,8 @@ def test_exports_every_declared_symbol(L):
 
 
 STRUCTS = {"kvq_decode_params": kvq.DecodeParams, "kvq_append_params": kvq.AppendParams,
-           "kvq_paged_decode_params": kvq.PagedDecodeParams, "kvq_paged_append_params": kvq.PagedAppendParams}
+           "kvq_paged_decode_params": kvq.PagedDecodeParams, "kvq_paged_append_params": kvq.PagedAppendParams,
+           "kvq_prefill_params": kvq.PrefillParams}
 
 
 def test_struct_layout_matches_c(tmp_path):
@@ -204,3 +205,17 @@ def test_paged_append_rejects_before_hip(L):
         q.update(bad)
         assert L.kvq_paged_append_launch(ctypes.byref(kvq.PagedAppendParams(**q)), None) == INVALID, bad
     assert L.kvq_paged_append_launch(None, None) == INVALID
+
+
+def test_prefill_rejects_before_hip(L):
+    ok = dict(batch=2, num_kv_heads=2, head_dim=128, tokens=16, dtype=0, k_new=FAKE, v_new=FAKE, start=None,
+              uniform_start=0, capacity=64, k_cache=FAKE, v_cache=FAKE, k_scale=FAKE, v_scale=FAKE,
+              block_table=None, page_size=0, num_pages=0, max_pages_per_seq=0)
+    for bad in (dict(batch=0), dict(head_dim=0), dict(head_dim=5000), dict(tokens=-1), dict(dtype=2),
+                dict(k_new=None), dict(v_scale=None), dict(capacity=0), dict(block_table=FAKE),
+                dict(block_table=FAKE, page_size=16, num_pages=4, max_pages_per_seq=0),
+                dict(batch=1 << 16, num_kv_heads=1 << 8, tokens=1 << 8)):
+        q = dict(ok)
+        q.update(bad)
+        assert L.kvq_prefill_quantize_launch(ctypes.byref(kvq.PrefillParams(**q)), None) == INVALID, bad
+    assert L.kvq_prefill_quantize_launch(None, None) == INVALID
