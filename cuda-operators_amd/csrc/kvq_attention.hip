@@ -1,0 +1,356 @@
+// kvq_attention.hip -- dense fp32 attention forward on gfx950 matrix cores:
+// out = softmax(Q K^T / sqrt(d)) V for Q[M,d], K/V[N,d] (one head), the math
+// of the reference's attention_online_launch (attention/softmax_new.cu:87-281).
+//
+// attention_mfma<D> (d in {32, 64, 128}): a workgroup of 8 waves owns 128
+// queries (16 per wave) and one split of the keys, which it streams through
+// LDS in 64-key tiles shared by all its waves.  Both products run on
+// v_mfma_f32_16x16x4_f32 (fp32 in, fp32 accumulate: the same arithmetic as
+// fp32 FMAs, in another order):
+//   * S^T = K Q^T per 16-key block: A = K rows from LDS, B = this wave's q
+//     (held in registers, pre-scaled by softmax_scale * log2 e); the k index
+//     g = lane / 16 of step s is dim g * D/4 + s, so each lane reads its K
+//     operands as contiguous 16-byte LDS loads.  C leaves lane l with keys
+//     4g + i of query l % 16.
+//   * online softmax per query: max and sum over the lane's 16 keys of the
+//     tile and across the 4 lane groups (shuffles); exp2 of log2-unit scores.
+//   * O^T += V^T P^T: the P values stay in the registers the QK product left
+//     them in -- step i of a key block takes register i of every lane, i.e.
+//     keys {4g + i}, and the A operand reads V rows 4g + i to match.  Output
+//     rows (dims) of block c are dims (D/16) * m + c, so each lane's V
+//     operands are contiguous too.
+// Keys are split over the grid's second dimension when the query blocks alone
+// cannot fill the GPU; splits write partial (m, l, acc) records and a second
+// launch, attention_merge, combines them over the whole grid (a merge by the
+// last split to arrive would leave the records of a query block to one CU,
+// whose far reads then dominate the launch).
+//
+// attention_generic: any d <= 1024 (one wave per query row, VALU), the
+// correctness path for other head dims.
+#include <math.h>
+
+#include "kvq_device.hpp"
+#include "kvq_internal.hpp"
+
+namespace kvq {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kAWaves = 8;              // waves per workgroup, 16 queries each
+constexpr int kAQ = 16 * kAWaves;       // queries per workgroup
+constexpr int kAK = 64;                 // keys per LDS tile
+constexpr int kAttnMaxSplits = 1024;    // key splits per launch (the merge loops over them)
+
+// Merge of the split records: a group of 2^glog lanes (within one wave) per
+// (query, 16-byte output column), lane j of the group taking splits j, j + G,
+// ...  The weights of a query's splits, w_s = 2^(m_s - max m), come from its
+// (m, l) records (read by every column group of the query: cache hits after
+// the first); out = sum_s w_s acc_s / sum_s w_s l_s, reduced over the group
+// with shuffles.  The host picks G so that a lane sees at most 8 splits.
+constexpr int kMergeThreads = 256;
+template <int D>
+__global__ __launch_bounds__(kMergeThreads) void attention_merge(const AttnArgs a, int glog) {
+    constexpr int C4 = D / 4;
+    const int G = 1 << glog;
+    const int j = threadIdx.x & (G - 1);
+    const int e = (blockIdx.x * kMergeThreads + threadIdx.x) >> glog;
+    if (e >= a.M * C4) return;  // whole groups leave together
+    const int q = e / C4;
+    const int S = a.splits;
+    const float2* ml = reinterpret_cast<const float2*>(a.part_ml) + q;
+    const float4* acc = reinterpret_cast<const float4*>(a.part_acc) + e;
+    const size_t ml_stride = static_cast<size_t>(a.M);
+    const size_t acc_stride = static_cast<size_t>(a.M) * C4;
+    float mx = -INFINITY;
+    for (int sp = j; sp < S; sp += G) mx = fmaxf(mx, ml[sp * ml_stride].x);
+    for (int off = 1; off < G; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    const float ms = mx == -INFINITY ? 0.0f : mx;
+    float L = 0.0f;
+    float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s0 = j; s0 < S; s0 += 8 * G) {
+        float4 x[8];
+        float2 y[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const size_t sp = static_cast<size_t>(min(s0 + u * G, S - 1));
+            x[u] = acc[sp * acc_stride];
+            y[u] = ml[sp * ml_stride];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float w = s0 + u * G < S ? fast_exp2(y[u].x - ms) : 0.0f;
+            L = fmaf(y[u].y, w, L);
+            A.x = fmaf(x[u].x, w, A.x);
+            A.y = fmaf(x[u].y, w, A.y);
+            A.z = fmaf(x[u].z, w, A.z);
+            A.w = fmaf(x[u].w, w, A.w);
+        }
+    }
+    for (int off = 1; off < G; off <<= 1) {
+        L += __shfl_xor(L, off);
+        A.x += __shfl_xor(A.x, off);
+        A.y += __shfl_xor(A.y, off);
+        A.z += __shfl_xor(A.z, off);
+        A.w += __shfl_xor(A.w, off);
+    }
+    if (j == 0) {
+        const float inv = 1.0f / L;
+        reinterpret_cast<float4*>(a.out)[e] = make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs a) {
+    constexpr int DQ = D / 4;   // contraction dims per lane group in QK
+    constexpr int NB = D / 16;  // 16-dim output blocks; block c row m = dim NB * m + c
+    static_assert(NB % 4 == 0 || NB == 2, "V operand / output vector width");
+    constexpr int KS = D + 4;   // LDS row stride in floats (16-byte pad: conflict-free row reads)
+    constexpr int NL = kAK * D / 4 / (kAWaves * kWave);  // float4 per thread per tile per tensor
+    static_assert(NL >= 1, "tile load shape");
+    __shared__ __align__(16) float s_kv[2 * kAK * KS];  // K tile, V tile
+    float* const s_k = s_kv;
+    float* const s_v = s_kv + kAK * KS;
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int split = blockIdx.y;
+    const int q0 = blockIdx.x * kAQ + wave * 16;
+    const int k0 = split * a.chunk;
+    const int k1 = min(a.N, k0 + a.chunk);
+
+    // This wave's q^T operand: lane holds q[q0 + r][g * DQ + s], scaled.
+    float qv[DQ];
+    {
+        const float* qp = a.q + static_cast<size_t>(min(q0 + r, a.M - 1)) * D + g * DQ;
+#pragma unroll
+        for (int j = 0; j < DQ / 4; j++) {
+            const float4 x = *reinterpret_cast<const float4*>(qp + 4 * j);
+            qv[4 * j] = x.x * a.scale_log2;
+            qv[4 * j + 1] = x.y * a.scale_log2;
+            qv[4 * j + 2] = x.z * a.scale_log2;
+            qv[4 * j + 3] = x.w * a.scale_log2;
+        }
+    }
+    f32x4 o[NB];
+#pragma unroll
+    for (int c = 0; c < NB; c++) o[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+
+    // Tile loads: float4 f = threadIdx.x + j * 512 of the 64 x D tile.
+    float4 pk[NL], pv[NL];
+    auto load_tile = [&](int t0) {
+#pragma unroll
+        for (int j = 0; j < NL; j++) {
+            const int f = threadIdx.x + j * kAWaves * kWave;
+            const int row = f / (D / 4);
+            const int c4 = f - row * (D / 4);
+            const int key = t0 + row;
+            // Rows past the split's end read its last row (in bounds) and are
+            // zeroed by a select.
+            const size_t kr = static_cast<size_t>(min(key, k1 - 1)) * D + 4 * c4;
+            const float keep = key < k1 ? 1.0f : 0.0f;
+            const float4 x = *reinterpret_cast<const float4*>(a.k + kr);
+            const float4 y = *reinterpret_cast<const float4*>(a.v + kr);
+            pk[j] = make_float4(x.x * keep, x.y * keep, x.z * keep, x.w * keep);
+            pv[j] = make_float4(y.x * keep, y.y * keep, y.z * keep, y.w * keep);
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int j = 0; j < NL; j++) {
+            const int f = threadIdx.x + j * kAWaves * kWave;
+            const int row = f / (D / 4);
+            const int c4 = f - row * (D / 4);
+            *reinterpret_cast<float4*>(s_k + row * KS + 4 * c4) = pk[j];
+            *reinterpret_cast<float4*>(s_v + row * KS + 4 * c4) = pv[j];
+        }
+    };
+
+    if (k0 < k1) load_tile(k0);
+    for (int t0 = k0; t0 < k1; t0 += kAK) {
+        __syncthreads();  // every wave is done with the previous tile
+        store_tile();
+        __syncthreads();
+        if (t0 + kAK < k1) load_tile(t0 + kAK);  // the next tile is in flight during compute
+
+        // S^T for the 4 key blocks: sv[4 kb + i] = score of key t0 + 16 kb + 4 g + i, query r.
+        float sv[16];
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) {
+            f32x4 c = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const float* kr = s_k + (16 * kb + r) * KS + g * DQ;
+#pragma unroll
+            for (int s4 = 0; s4 < DQ; s4 += 4) {
+                const float4 kk = *reinterpret_cast<const float4*>(kr + s4);
+                c = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, qv[s4], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, qv[s4 + 1], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qv[s4 + 2], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qv[s4 + 3], c, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int key = t0 + 16 * kb + 4 * g + i;
+                sv[4 * kb + i] = key < k1 ? c[i] : -INFINITY;
+            }
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 16; j++) mt = fmaxf(mt, sv[j]);
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        const float ms = mn == -INFINITY ? 0.0f : mn;
+        const float alpha = fast_exp2(m - ms);
+        m = mn;
+        l *= alpha;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            sv[j] = fast_exp2(sv[j] - ms);
+            l += sv[j];
+        }
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+            for (int c = 0; c < NB; c++) o[c] *= alpha;
+        }
+        // O^T += V^T P^T: step (kb, i) contracts keys 16 kb + 4 g + i (k index g).
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float* vr = s_v + (16 * kb + 4 * g + i) * KS + NB * r;
+                float vv[NB];
+                if constexpr (NB % 4 == 0) {
+#pragma unroll
+                    for (int c4 = 0; c4 < NB; c4 += 4) {
+                        const float4 x = *reinterpret_cast<const float4*>(vr + c4);
+                        vv[c4] = x.x;
+                        vv[c4 + 1] = x.y;
+                        vv[c4 + 2] = x.z;
+                        vv[c4 + 3] = x.w;
+                    }
+                } else {
+                    const float2 x = *reinterpret_cast<const float2*>(vr);
+                    vv[0] = x.x;
+                    vv[1] = x.y;
+                }
+#pragma unroll
+                for (int c = 0; c < NB; c++)
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[c], sv[4 * kb + i], o[c], 0, 0, 0);
+            }
+        }
+    }
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+
+    // One split: the normalised output.  Several: the partial record of
+    // (split, query) -- unnormalised acc, and (m, l) -- for attention_merge.
+    const int q = q0 + r;
+    if (q < a.M) {
+        const bool whole = a.splits == 1;
+        const float inv = whole ? 1.0f / l : 1.0f;
+        float* const row = whole ? a.out + static_cast<size_t>(q) * D
+                                 : a.part_acc + (static_cast<size_t>(split) * a.M + q) * D;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float* op = row + NB * (4 * g + i);
+            if constexpr (NB % 4 == 0) {
+#pragma unroll
+                for (int c4 = 0; c4 < NB; c4 += 4)
+                    *reinterpret_cast<float4*>(op + c4) = make_float4(o[c4][i] * inv, o[c4 + 1][i] * inv,
+                                                                      o[c4 + 2][i] * inv, o[c4 + 3][i] * inv);
+            } else {
+                *reinterpret_cast<float2*>(op) = make_float2(o[0][i] * inv, o[1][i] * inv);
+            }
+        }
+        if (!whole && g == 0)
+            *reinterpret_cast<float2*>(a.part_ml + (static_cast<size_t>(split) * a.M + q) * 2) = make_float2(m, l);
+    }
+}
+
+// Any d <= 1024: one wave per query row; scores of 64 keys per step, one per
+// lane (dot over d), online softmax over the steps, accumulator in LDS.
+constexpr int kGenWaves = 4;
+__global__ __launch_bounds__(kGenWaves* kWave) void attention_generic(const AttnArgs a) {
+    extern __shared__ float sh[];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int row = blockIdx.x * kGenWaves + wave;
+    const int d = a.d;
+    float* acc = sh + wave * d;
+    if (row >= a.M) return;
+    for (int j = lane; j < d; j += kWave) acc[j] = 0.0f;
+    const float* q = a.q + static_cast<size_t>(row) * d;
+    float m = -INFINITY, l = 0.0f;
+    for (int t0 = 0; t0 < a.N; t0 += kWave) {
+        const int t = t0 + lane;
+        float s = -INFINITY;
+        if (t < a.N) {
+            const float* k = a.k + static_cast<size_t>(t) * d;
+            float dot = 0.0f;
+            for (int j = 0; j < d; j++) dot = fmaf(q[j], k[j], dot);
+            s = dot * a.scale_log2;
+        }
+        const float mn = fmaxf(m, wave_max(s));
+        const float alpha = fast_exp2(m - mn);
+        const float p = fast_exp2(s - mn);
+        l = l * alpha + wave_sum(p);
+        m = mn;
+        const int nt = min(kWave, a.N - t0);
+        // Dims in passes of 64 with every lane active, so the shuffles read
+        // live lanes; lanes past d carry zeros and store nothing.
+        for (int j0 = 0; j0 < d; j0 += kWave) {
+            const int j = j0 + lane;
+            const bool in = j < d;
+            float x = in ? acc[j] * alpha : 0.0f;
+            for (int u = 0; u < nt; u++) {
+                const float pu = __shfl(p, u);
+                x = fmaf(pu, in ? a.v[static_cast<size_t>(t0 + u) * d + j] : 0.0f, x);
+            }
+            if (in) acc[j] = x;
+        }
+    }
+    for (int j = lane; j < d; j += kWave) a.out[static_cast<size_t>(row) * d + j] = acc[j] / l;
+}
+
+}  // namespace
+
+int attention_tuned_dim(int d) { return d == 32 || d == 64 || d == 128; }
+int attention_query_block() { return kAQ; }
+int attention_key_tile() { return kAK; }
+int attention_max_splits(int) { return kAttnMaxSplits; }
+
+hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
+    if (attention_tuned_dim(a.d)) {
+        const dim3 grid(static_cast<unsigned>((a.M + kAQ - 1) / kAQ), static_cast<unsigned>(a.splits));
+        const dim3 block(kAWaves * kWave);
+        int glog = 0;  // lanes per merge group: at most 8 splits per lane, at most a wave
+        while (glog < 6 && ((a.splits - 1) >> glog) >= 8) glog++;
+        const dim3 mgrid(static_cast<unsigned>(
+            ((static_cast<long long>(a.M) * (a.d / 4) << glog) + kMergeThreads - 1) / kMergeThreads));
+        const dim3 mblock(kMergeThreads);
+        switch (a.d) {
+            case 32:
+                hipLaunchKernelGGL(attention_mfma<32>, grid, block, 0, stream, a);
+                if (a.splits > 1) hipLaunchKernelGGL(attention_merge<32>, mgrid, mblock, 0, stream, a, glog);
+                break;
+            case 64:
+                hipLaunchKernelGGL(attention_mfma<64>, grid, block, 0, stream, a);
+                if (a.splits > 1) hipLaunchKernelGGL(attention_merge<64>, mgrid, mblock, 0, stream, a, glog);
+                break;
+            default:
+                hipLaunchKernelGGL(attention_mfma<128>, grid, block, 0, stream, a);
+                if (a.splits > 1) hipLaunchKernelGGL(attention_merge<128>, mgrid, mblock, 0, stream, a, glog);
+                break;
+        }
+        return hipGetLastError();
+    }
+    const dim3 grid(static_cast<unsigned>((a.M + kGenWaves - 1) / kGenWaves));
+    const size_t lds = sizeof(float) * kGenWaves * static_cast<size_t>(a.d);
+    hipLaunchKernelGGL(attention_generic, grid, dim3(kGenWaves * kWave), lds, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace kvq

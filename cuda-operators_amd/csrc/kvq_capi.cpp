@@ -9,6 +9,8 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <functional>
+#include <map>
 #include <mutex>
 
 #include "../../include/kvq.h"
@@ -300,6 +302,114 @@ DecodePlan paged_plan(const kvq_paged_decode_params* p) {
                      p->page_size, p->lengths != nullptr, p->num_splits, INT_MAX, true);
 }
 
+// ---- dense attention ------------------------------------------------------
+
+// Workgroups the attention grid should reach before keys are split: one
+// round of resident matrix-core workgroups (8 waves each; at d = 128 the
+// register file holds one per CU, below that two).
+int attention_target_workgroups(int d) { return d >= 128 ? 256 : 512; }
+
+struct AttnPlan {
+    bool tuned = false;
+    int splits = 1, chunk = 0;
+    size_t ml_bytes = 0, acc_bytes = 0;
+    size_t bytes() const { return ml_bytes + acc_bytes; }
+};
+
+bool attention_args_ok(int M, int N, int d, const void* q, const void* k, const void* v, const void* out) {
+    if (!q || !k || !v || !out) return false;
+    if (M <= 0 || N <= 0 || d <= 0 || d > 1024) return false;
+    // Key loops step 64 keys past N; keep those indices in int range.
+    return N <= INT_MAX - 1024 && M <= INT_MAX - 1024;
+}
+
+AttnPlan attention_plan(int M, int N, int d, bool aligned, int requested) {
+    AttnPlan p;
+    p.tuned = kvq::attention_tuned_dim(d) && aligned;
+    p.chunk = N;
+    if (!p.tuned) return p;  // the generic kernel runs unsplit
+    const int tile = kvq::attention_key_tile();
+    const long long qblocks = (static_cast<long long>(M) + kvq::attention_query_block() - 1) /
+                              kvq::attention_query_block();
+    const long long tiles = (static_cast<long long>(N) + tile - 1) / tile;
+    const long long target = attention_target_workgroups(d);
+    long long want = requested > 0 ? requested : (target + qblocks - 1) / qblocks;
+    want = std::max(1LL, std::min({want, tiles, static_cast<long long>(kvq::attention_max_splits(d))}));
+    // The merge runs up to 64 lanes per 16-byte output column, indexed in int.
+    if (static_cast<long long>(M) * (d / 4) * 64 >= INT_MAX) want = 1;
+    const long long chunk_tiles = (tiles + want - 1) / want;
+    p.chunk = static_cast<int>(std::min<long long>(chunk_tiles * tile, N));
+    p.splits = static_cast<int>((N + static_cast<long long>(p.chunk) - 1) / p.chunk);
+    if (p.splits > 1) {
+        p.ml_bytes = round_up(static_cast<size_t>(p.splits) * M * 2 * sizeof(float), kAlign);
+        p.acc_bytes = round_up(static_cast<size_t>(p.splits) * M * d * sizeof(float), kAlign);
+    }
+    return p;
+}
+
+bool attention_aligned(const float* q, const float* k, const float* v, const float* out) {
+    return aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
+}
+
+hipError_t attention_run(int M, int N, int d, const float* q, const float* k, const float* v, float* out,
+                         float scale, const AttnPlan& p, void* ws, hipStream_t stream) {
+    kvq::AttnArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    a.M = M;
+    a.N = N;
+    a.d = d;
+    a.splits = p.splits;
+    a.chunk = p.chunk;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    if (p.splits > 1) {
+        char* base = static_cast<char*>(ws);
+        a.part_ml = reinterpret_cast<float*>(base);
+        a.part_acc = reinterpret_cast<float*>(base + p.ml_bytes);
+    }
+    return kvq::launch_attention(a, stream);
+}
+
+// Library-owned attention workspaces, one per (device, stream): launches on
+// one stream are ordered and may share one; different streams must not.
+// Grown on demand (hipFree waits for in-flight work); the split records need
+// no initial contents.
+struct AttnWorkspaceKey {
+    int device;
+    hipStream_t stream;
+    bool operator<(const AttnWorkspaceKey& o) const {
+        return device != o.device ? device < o.device : std::less<hipStream_t>()(stream, o.stream);
+    }
+};
+std::mutex g_attn_ws_mutex;
+std::map<AttnWorkspaceKey, SolveWorkspace> g_attn_ws;
+
+hipError_t attention_workspace(size_t need, hipStream_t stream, void** out) {
+    *out = nullptr;
+    if (need == 0) return hipSuccess;
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    std::lock_guard<std::mutex> lock(g_attn_ws_mutex);
+    SolveWorkspace& w = g_attn_ws[AttnWorkspaceKey{dev, stream}];
+    if (w.bytes < need) {
+        if (w.ptr) {
+            err = hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.bytes = 0;
+            if (err != hipSuccess) return err;
+        }
+        const size_t bytes = round_up(need, 1 << 20);
+        err = hipMalloc(&w.ptr, bytes);
+        if (err != hipSuccess) return err;
+        w.bytes = bytes;
+    }
+    *out = w.ptr;
+    return hipSuccess;
+}
+
 }  // namespace
 
 extern "C" {
@@ -510,6 +620,33 @@ hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t 
     const bool vec_ok = aligned16(p->k_new) && aligned16(p->v_new) &&
                         ((reinterpret_cast<uintptr_t>(p->k_cache) | reinterpret_cast<uintptr_t>(p->v_cache)) & 7u) == 0;
     return kvq::launch_prefill(a, p->head_dim, p->dtype == KVQ_DTYPE_BF16, vec_ok, stream);
+}
+
+hipError_t attention_online_launch(const float* Q, const float* K, const float* V, float* output, int M, int N,
+                                   int d, hipStream_t stream) {
+    if (!attention_args_ok(M, N, d, Q, K, V, output)) return hipErrorInvalidValue;
+    const AttnPlan p = attention_plan(M, N, d, attention_aligned(Q, K, V, output), 0);
+    void* ws = nullptr;
+    const hipError_t err = attention_workspace(p.bytes(), stream, &ws);
+    if (err != hipSuccess) return err;
+    return attention_run(M, N, d, Q, K, V, output, 1.0f / sqrtf(static_cast<float>(d)), p, ws, stream);
+}
+
+size_t kvq_attention_workspace_size(const kvq_attention_params* p) {
+    if (!p || !attention_args_ok(p->M, p->N, p->d, p->q, p->k, p->v, p->out) || p->num_splits < 0) return 0;
+    return attention_plan(p->M, p->N, p->d, attention_aligned(p->q, p->k, p->v, p->out), p->num_splits).bytes();
+}
+
+hipError_t kvq_attention_launch(const kvq_attention_params* p, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream) {
+    if (!p || !attention_args_ok(p->M, p->N, p->d, p->q, p->k, p->v, p->out) || p->num_splits < 0)
+        return hipErrorInvalidValue;
+    const AttnPlan plan =
+        attention_plan(p->M, p->N, p->d, attention_aligned(p->q, p->k, p->v, p->out), p->num_splits);
+    if (plan.bytes() > 0 && (!workspace || workspace_bytes < plan.bytes() || !aligned16(workspace)))
+        return hipErrorInvalidValue;
+    const float scale = p->softmax_scale != 0.0f ? p->softmax_scale : 1.0f / sqrtf(static_cast<float>(p->d));
+    return attention_run(p->M, p->N, p->d, p->q, p->k, p->v, p->out, scale, plan, workspace, stream);
 }
 
 const char* kvq_version(void) { return "kvq 0.1.0 gfx950"; }

@@ -130,6 +130,24 @@ struct PrefillArgs {
 hipError_t launch_prefill(const PrefillArgs& a, int d, bool bf16, bool vec_ok, hipStream_t stream);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 
+// Dense fp32 attention (kvq_attention.hip): out = softmax(q k^T * scale) v.
+struct AttnArgs {
+    const float* q;    // [M, d]
+    const float* k;    // [N, d]
+    const float* v;    // [N, d]
+    float* out;        // [M, d]
+    float* part_ml;    // [splits, M, 2] partial (max in log2 units, sum)
+    float* part_acc;   // [splits, M, d] unnormalised partial accumulators
+    int M, N, d;
+    int splits, chunk;  // key splits (grid y) and keys per split (a multiple of the key tile)
+    float scale_log2;   // softmax scale * log2(e)
+};
+int attention_tuned_dim(int d);   // the matrix-core kernel handles head dim d
+int attention_query_block();      // queries per matrix-core workgroup
+int attention_key_tile();         // keys per LDS tile
+int attention_max_splits(int d);  // most key splits per matrix-core launch (tuned d)
+hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
+
 // Tokens one workgroup iteration of the fast kernel covers for head dim d and
 // sg query heads per workgroup; 0 when the fast kernel does not support d.
 int fast_tile_tokens(int d, int sg);

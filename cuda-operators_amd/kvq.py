@@ -91,10 +91,19 @@ class PrefillParams(ctypes.Structure):
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 
+
+class AttentionParams(ctypes.Structure):
+    """struct kvq_attention_params (include/kvq.h)."""
+    _fields_ = [
+        ("M", _int), ("N", _int), ("d", _int), ("q", _vp), ("k", _vp), ("v", _vp), ("out", _vp),
+        ("softmax_scale", ctypes.c_float), ("num_splits", _int),
+    ]
+
 EXPORTS = ("solve", "kv_int8_split_launch", "kv_int8_simple_launch", "kvq_decode_workspace_size",
            "kvq_workspace_init", "kvq_decode_launch", "kvq_append_launch", "kvq_quantize_rows_launch",
            "kvq_paged_decode_workspace_size", "kvq_paged_decode_launch", "kvq_paged_append_launch",
-           "kvq_prefill_quantize_launch", "kvq_version")
+           "kvq_prefill_quantize_launch", "attention_online_launch", "kvq_attention_workspace_size",
+           "kvq_attention_launch", "kvq_version")
 
 
 class KvqError(RuntimeError):
@@ -136,6 +145,12 @@ def lib() -> ctypes.CDLL:
         L.kvq_paged_append_launch.restype = _int
         L.kvq_prefill_quantize_launch.argtypes = [ctypes.POINTER(PrefillParams), _vp]
         L.kvq_prefill_quantize_launch.restype = _int
+        L.attention_online_launch.argtypes = [_vp, _vp, _vp, _vp, _int, _int, _int, _vp]
+        L.attention_online_launch.restype = _int
+        L.kvq_attention_workspace_size.argtypes = [ctypes.POINTER(AttentionParams)]
+        L.kvq_attention_workspace_size.restype = ctypes.c_size_t
+        L.kvq_attention_launch.argtypes = [ctypes.POINTER(AttentionParams), _vp, ctypes.c_size_t, _vp]
+        L.kvq_attention_launch.restype = _int
         L.kvq_version.restype = ctypes.c_char_p
         _lib = L
         return L
@@ -380,6 +395,52 @@ def prefill(k_new, v_new, k_cache, v_cache, k_scale, v_scale, start=None, unifor
     _check("kvq_prefill_quantize_launch", lib().kvq_prefill_quantize_launch(ctypes.byref(p), _stream(stream)))
 
 
+def _attention_shapes(q, k, v, out):
+    M, d = q.shape
+    N = k.shape[0]
+    _need(q, torch.float32, (M, d), "q")
+    _need(k, torch.float32, (N, d), "k")
+    _need(v, torch.float32, (N, d), "v")
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, torch.float32, (M, d), "out")
+    return M, N, d, out
+
+
+def attention_online(q, k, v, out=None, stream=None) -> torch.Tensor:
+    """softmax(q k^T / sqrt(d)) v through the reference ABI (attention_online_launch):
+    q [M, d], k/v [N, d] fp32; split workspaces are owned by the library."""
+    M, N, d, out = _attention_shapes(q, k, v, out)
+    _check("attention_online_launch",
+           lib().attention_online_launch(_ptr(q), _ptr(k), _ptr(v), _ptr(out), M, N, d, _stream(stream)))
+    return out
+
+
+def attention_params(q, k, v, out, softmax_scale: float = 0.0, num_splits: int = 0) -> AttentionParams:
+    M, N, d, out = _attention_shapes(q, k, v, out)
+    return AttentionParams(M, N, d, _ptr(q), _ptr(k), _ptr(v), _ptr(out), float(softmax_scale), int(num_splits))
+
+
+def attention_workspace_size(p: AttentionParams) -> int:
+    return int(lib().kvq_attention_workspace_size(ctypes.byref(p)))
+
+
+def attention(q, k, v, out=None, softmax_scale: float = 0.0, num_splits: int = 0, workspace=None,
+              stream=None) -> torch.Tensor:
+    """softmax(q k^T * scale) v (kvq_attention_launch) with a caller-owned
+    workspace (allocated here when none is given)."""
+    if out is None:
+        out = torch.empty_like(q)
+    p = attention_params(q, k, v, out, softmax_scale, num_splits)
+    n = attention_workspace_size(p)
+    if n and workspace is None:
+        workspace = torch.empty(n, dtype=torch.uint8, device=q.device)
+    nb = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check("kvq_attention_launch", lib().kvq_attention_launch(ctypes.byref(p), _ptr(workspace), nb,
+                                                              _stream(stream)))
+    return out
+
+
 def default_softmax_scale(d: int) -> float:
     """1/sqrtf(d) in fp32, as kv_cache/KV_int8_split_optimized.cu:335."""
     import numpy as np
@@ -396,4 +457,5 @@ __all__ = ["lib", "version", "solve", "kv_int8_split_launch", "DecodeParams", "A
            "decode", "decode_params", "decode_launch", "workspace_size", "workspace_init", "new_workspace",
            "append", "quantize_rows", "kv_bytes", "KvqError", "EXPORTS", "PagedDecodeParams",
            "PagedAppendParams", "PagedDecoder", "paged_append", "PrefillParams", "prefill", "DTYPE_F32",
-           "DTYPE_BF16"]
+           "DTYPE_BF16", "AttentionParams", "attention_online", "attention_params", "attention_workspace_size",
+           "attention"]

@@ -241,6 +241,46 @@ typedef struct kvq_prefill_params {
 /* One launch quantises all B*Hkv*L K and V rows. */
 hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t stream);
 
+/* ============ Part 5: dense fp32 attention (prefill-shaped) ============
+ *
+ * out[M, d] = softmax(Q K^T * scale) V for Q[M, d], K/V[N, d] fp32, one head,
+ * no mask; the operator of attention/softmax_new.cu:87-281.  Inputs must be
+ * finite (as the reference requires, attention/softmax_new.cu:237). */
+
+/* Replaces attention_online_launch (attention/softmax_new.cu:239-281): same
+ * arguments, scale 1/sqrtf(d), hipErrorInvalidValue for a NULL pointer,
+ * M, N or d <= 0, or d > 1024 (the reference's limit, :252).  When the
+ * queries alone cannot fill the GPU the keys are split over workgroups; the
+ * partial results then live in a workspace the library owns, one per (device,
+ * stream), allocated on first use and grown on demand (hipMalloc).  Callers
+ * that must not allocate use kvq_attention_launch with their own workspace.
+ * The reference's compatibility `solve(Q, K, V, output, M, N, d)`
+ * (attention/softmax_new.cu:283-287) is not exported: its symbol is the
+ * decode `solve` above. */
+hipError_t attention_online_launch(const float* Q, const float* K, const float* V, float* output, int M, int N,
+                                   int d, hipStream_t stream);
+
+typedef struct kvq_attention_params {
+    int M, N, d;              /* queries, keys, head dim (1 <= d <= 1024) */
+    const float* q;           /* [M, d] */
+    const float* k;           /* [N, d] */
+    const float* v;           /* [N, d] */
+    float* out;               /* [M, d] */
+    float softmax_scale;      /* 0 -> 1/sqrtf(d) */
+    int num_splits;           /* 0 -> chosen by the library; else a request (clamped) */
+} kvq_attention_params;
+
+/* Workspace bytes kvq_attention_launch needs for p (0: none, or invalid p):
+ * the split records, which need no initial contents. */
+size_t kvq_attention_workspace_size(const kvq_attention_params* p);
+
+/* attention_online_launch with an explicit scale, split request and
+ * caller-owned workspace; allocates nothing.  With splits, a second kernel
+ * merges the records.  Launches that share a workspace must be ordered (one
+ * stream). */
+hipError_t kvq_attention_launch(const kvq_attention_params* p, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream);
+
 /* Library version string, e.g. "kvq 0.1.0 gfx950". */
 const char* kvq_version(void);
 

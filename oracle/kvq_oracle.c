@@ -27,6 +27,8 @@
  *                         underflows to 0) gives scale 0 and all-zero int8.
  *   kvq_ref_append        writes one quantised token per (b, kv_head) at
  *                         positions[b] into the cache (layout [B,Hkv,cap,d]).
+ *   kvq_ref_attention_f32 dense fp32 attention softmax(Q K^T / sqrt(d)) V, the
+ *                         math of attention/softmax_new.cu:87-281.
  *
  * Pinning (what checks this oracle, in tests/test_oracle.py):
  *   - float64 textbook softmax attention (numpy/scipy) on random inputs,
@@ -64,6 +66,8 @@
 #define PLANT_ROUND_AWAY 7  /* roundf (half away from zero) instead of rintf */
 #define PLANT_TRUNC 8       /* truncation instead of rounding               */
 #define PLANT_NO_VSCALE 9   /* value dequant drops v_scale                  */
+#define PLANT_ATT_INV_D 10  /* dense attention: 1/d instead of 1/sqrt(d)     */
+#define PLANT_ATT_V_T 11    /* dense attention: V indexed [d][n]             */
 
 int kvq_ref_plant_id(void) { return PLANT; }
 
@@ -285,5 +289,55 @@ void kvq_ref_append(const float* k_new, const float* v_new, int8_t* k, int8_t* v
             quantize_row(k_new + row * d, d, k + tok * d, ks + tok);
             quantize_row(v_new + row * d, d, v + tok * d, vs + tok);
         }
+    }
+}
+
+/* Dense fp32 attention, one query row per call: the math of the reference's
+ * attention_online_launch (attention/softmax_new.cu:87-203, launch :239-281):
+ * s_t = (sum_i fmaf(q_i, K[t,i])) * (1/sqrtf(d)), m = max_t s_t,
+ * e_t = expf(s_t - m), l = sum_t e_t, out_j = (sum_t fmaf(e_t, V[t,j])) * (1/l)
+ * (the reference scales the accumulator by a reciprocal of l, :192-200).
+ * Sums are sequential in t and i. */
+static void attention_row_f32(const float* q, const float* K, const float* V, float* out, int N, int d,
+                              float* e) {
+#if PLANT == PLANT_ATT_INV_D
+    const float scale = 1.0f / (float)d;
+#else
+    const float scale = 1.0f / sqrtf((float)d);
+#endif
+    float m = -FLT_MAX;
+    for (int t = 0; t < N; t++) {
+        float dot = 0.0f;
+        for (int i = 0; i < d; i++) dot = fmaf(q[i], K[(size_t)t * d + i], dot);
+        e[t] = dot * scale;
+        m = fmaxf(m, e[t]);
+    }
+    float l = 0.0f;
+    for (int t = 0; t < N; t++) {
+        e[t] = expf(e[t] - m);
+        l += e[t];
+    }
+    const float inv_l = 1.0f / l;
+    for (int j = 0; j < d; j++) {
+        float acc = 0.0f;
+        for (int t = 0; t < N; t++) {
+#if PLANT == PLANT_ATT_V_T
+            acc = fmaf(e[t], V[(size_t)j * N + t], acc);
+#else
+            acc = fmaf(e[t], V[(size_t)t * d + j], acc);
+#endif
+        }
+        out[j] = acc * inv_l;
+    }
+}
+
+/* Q[M,d], K[N,d], V[N,d] fp32 -> out[M,d]; OpenMP over query rows. */
+void kvq_ref_attention_f32(const float* Q, const float* K, const float* V, float* out, int M, int N, int d) {
+#pragma omp parallel
+    {
+        float* e = (float*)malloc(sizeof(float) * (size_t)(N > 0 ? N : 1));
+#pragma omp for schedule(static)
+        for (int r = 0; r < M; r++) attention_row_f32(Q + (size_t)r * d, K, V, out + (size_t)r * d, N, d, e);
+        free(e);
     }
 }

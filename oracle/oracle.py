@@ -64,6 +64,9 @@ def _load(path: str) -> ctypes.CDLL:
                                        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_int]
         lib.kvq_ref_append.restype = None
+        lib.kvq_ref_attention_f32.argtypes = [_c_f32p, _c_f32p, _c_f32p, _c_f32p, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int]
+        lib.kvq_ref_attention_f32.restype = None
         lib.kvq_ref_plant_id.restype = ctypes.c_int
         lib.kvq_ref_max_threads.restype = ctypes.c_int
         _libs[path] = lib
@@ -131,6 +134,18 @@ class Oracle:
     def decode_f64(self, q, k, v, ks, vs, lengths=None, uniform_len=None) -> np.ndarray:
         return self._decode(self.lib.kvq_ref_decode_f64, np.float64, q, k, v, ks, vs, lengths,
                             uniform_len)
+
+    # -- dense attention -------------------------------------------------------
+    def attention_f32(self, Q, K, V) -> np.ndarray:
+        """softmax(Q K^T / sqrt(d)) V for Q[M,d], K/V[N,d] fp32 (attention/softmax_new.cu)."""
+        Q, K, V = _c(Q, np.float32), _c(K, np.float32), _c(V, np.float32)
+        M, d = Q.shape
+        N = K.shape[0]
+        assert K.shape == (N, d) == V.shape
+        out = np.empty((M, d), np.float32)
+        self.lib.kvq_ref_attention_f32(_p(Q, _c_f32p), _p(K, _c_f32p), _p(V, _c_f32p), _p(out, _c_f32p),
+                                       M, N, d)
+        return out
 
     # -- quantiser -----------------------------------------------------------
     def quantize_rows(self, x):

@@ -257,9 +257,63 @@ def pin_append(oracle):
     return fails
 
 
+def textbook_attention_f64(Q, K, V):
+    """softmax(Q K^T / sqrt(d)) V in float64 with scipy's softmax."""
+    from scipy.special import softmax
+    Q, K, V = (np.asarray(x, np.float64) for x in (Q, K, V))
+    return softmax(Q @ K.T / np.sqrt(Q.shape[1]), axis=1) @ V
+
+
+def pin_attention_textbook(oracle):
+    """Dense fp32 attention (attention/softmax_new.cu) against the float64
+    textbook on random and heavy-tailed data, several shapes."""
+    fails = []
+    for seed, (M, N, d) in zip(SEEDS, ((7, 300, 64), (33, 129, 128), (5, 1000, 96))):
+        rng = np.random.default_rng(seed)
+        Q = rng.standard_normal((M, d)).astype(np.float32)
+        K = (rng.standard_t(4, (N, d)) * 0.7).astype(np.float32)
+        V = rng.standard_normal((N, d)).astype(np.float32)
+        got = oracle.attention_f32(Q, K, V)
+        ok, msg = close_report(got, textbook_attention_f64(Q, K, V), TIGHT_ATOL, TIGHT_RTOL)
+        if not ok:
+            fails.append(f"attention textbook {(M, N, d)}: {msg}")
+    return fails
+
+
+def pin_attention_closed_forms(oracle):
+    fails = []
+    rng = np.random.default_rng(8)
+    M, N, d = 4, 60, 32
+    Q = rng.standard_normal((M, d)).astype(np.float32)
+    V = rng.standard_normal((N, d)).astype(np.float32)
+    # N = 1: every output row is the V row.
+    got = oracle.attention_f32(Q, rng.standard_normal((1, d)).astype(np.float32), V[:1])
+    if not np.array_equal(got, np.repeat(V[:1], M, axis=0)):
+        fails.append("attention N=1 is not the V row")
+    # K = 0: uniform weights, the mean of V.
+    got = oracle.attention_f32(Q, np.zeros((N, d), np.float32), V)
+    ok, msg = close_report(got, np.repeat(V.astype(np.float64).mean(0, keepdims=True), M, 0), 1e-6, 1e-5)
+    if not ok:
+        fails.append(f"attention K=0 mean: {msg}")
+    # One dominating key: output -> that V row.
+    K = np.zeros((N, d), np.float32)
+    K[11] = 40.0
+    got = oracle.attention_f32(np.abs(Q) + 1.0, K, V)
+    ok, msg = close_report(got, np.repeat(V[11:12].astype(np.float64), M, 0), 1e-6, 1e-6)
+    if not ok:
+        fails.append(f"attention dominating key: {msg}")
+    # Key permutation invariance.
+    K = rng.standard_normal((N, d)).astype(np.float32)
+    perm = rng.permutation(N)
+    ok, msg = close_report(oracle.attention_f32(Q, K[perm], V[perm]), oracle.attention_f32(Q, K, V), 1e-6, 1e-5)
+    if not ok:
+        fails.append(f"attention permutation: {msg}")
+    return fails
+
+
 ALL_PINS = (pin_textbook_mha, pin_textbook_gqa_ragged, pin_selftest_kat, pin_closed_forms,
             pin_gqa_equals_replicated, pin_ragged_equals_truncated, pin_quantizer_properties,
-            pin_append)
+            pin_append, pin_attention_textbook, pin_attention_closed_forms)
 
 
 def run_all(oracle):

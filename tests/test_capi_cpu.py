@@ -45,7 +45,7 @@ def test_exports_every_declared_symbol(L):
 
 STRUCTS = {"kvq_decode_params": kvq.DecodeParams, "kvq_append_params": kvq.AppendParams,
            "kvq_paged_decode_params": kvq.PagedDecodeParams, "kvq_paged_append_params": kvq.PagedAppendParams,
-           "kvq_prefill_params": kvq.PrefillParams}
+           "kvq_prefill_params": kvq.PrefillParams, "kvq_attention_params": kvq.AttentionParams}
 
 
 def test_struct_layout_matches_c(tmp_path):
@@ -219,3 +219,35 @@ def test_prefill_rejects_before_hip(L):
         q.update(bad)
         assert L.kvq_prefill_quantize_launch(ctypes.byref(kvq.PrefillParams(**q)), None) == INVALID, bad
     assert L.kvq_prefill_quantize_launch(None, None) == INVALID
+
+
+@pytest.mark.parametrize("bad", [dict(q=None), dict(k=None), dict(v=None), dict(out=None), dict(M=0), dict(N=0),
+                                 dict(d=0), dict(M=-1), dict(N=-3), dict(d=-8), dict(d=1025)],
+                         ids=lambda b: ",".join(f"{k}={v}" for k, v in b.items()))
+def test_attention_rejects_before_hip(L, bad):
+    """attention_online_launch's checks (attention/softmax_new.cu:246-254)."""
+    a = dict(q=FAKE, k=FAKE, v=FAKE, out=FAKE, M=256, N=512, d=64)
+    a.update(bad)
+    assert L.attention_online_launch(a["q"], a["k"], a["v"], a["out"], a["M"], a["N"], a["d"], None) == INVALID
+    p = kvq.AttentionParams(a["M"], a["N"], a["d"], a["q"], a["k"], a["v"], a["out"], 0.0, 0)
+    assert L.kvq_attention_workspace_size(ctypes.byref(p)) == 0
+    assert L.kvq_attention_launch(ctypes.byref(p), FAKE, 1 << 30, None) == INVALID
+
+
+def test_attention_workspace_plan(L):
+    """Few query blocks split the keys (partial records); many query blocks,
+    one split, an untuned head dim or a misaligned pointer need none."""
+    def size(M, N, d, splits=0, q=FAKE):
+        return L.kvq_attention_workspace_size(ctypes.byref(kvq.AttentionParams(M, N, d, q, FAKE, FAKE, FAKE, 0.0,
+                                                                                splits)))
+    n = size(128, 8192, 128)
+    assert n >= 2 * 128 * (128 + 2) * 4
+    assert L.kvq_attention_launch(ctypes.byref(kvq.AttentionParams(128, 8192, 128, FAKE, FAKE, FAKE, FAKE, 0.0, 0)),
+                                  FAKE, n - 1, None) == INVALID
+    assert size(128 * 1024, 4096, 128) == 0
+    assert size(128, 8192, 128, splits=1) == 0
+    assert size(128, 8192, 96) == 0
+    assert size(128, 8192, 128, q=FAKE + 4) == 0
+    assert size(128, 64, 128) == 0  # one key tile: nothing to split
+    # A requested split count is clamped to whole key tiles.
+    assert size(128, 8192, 64, splits=1 << 20) == size(128, 8192, 64, splits=8192 // 64) > 0

@@ -1,0 +1,155 @@
+"""Dense fp32 attention (attention_online_launch / kvq_attention_launch) on the
+GPU, through the C ABI, against the oracle's restatement of
+attention/softmax_new.cu (kvq_ref_attention_f32, pinned in test_oracle.py).
+
+Tolerance: |gpu - oracle| <= 1e-4 + 1e-3 * |oracle| per element (fp32 with a
+different summation order and exp2 of log2-scaled scores).  Cases: the
+matrix-core head dims (32, 64, 128) with query counts around the 128-query
+block and key counts around the 64-key tile, split and unsplit plans,
+explicit split requests, untuned head dims and misaligned pointers (generic
+kernel), peaked and flat softmax, workspace reuse across calls, a side
+stream, and at full prefill size a float64 check of sampled rows."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import _gpu
+from _gpu import down, kvq, up
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+ATOL, RTOL = 1e-4, 1e-3
+
+
+@pytest.fixture(scope="module")
+def o():
+    return orc.get()
+
+
+def _problem(rng, M, N, d, qscale=1.0):
+    q = (rng.standard_normal((M, d)) * qscale).astype(np.float32)
+    k = rng.standard_normal((N, d)).astype(np.float32)
+    v = rng.standard_normal((N, d)).astype(np.float32)
+    return q, k, v
+
+
+def _close(got, ref, what=""):
+    np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL, err_msg=what)
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("M,N", [(1, 1), (1, 4099), (7, 64), (128, 65), (129, 300), (200, 1000), (256, 4096),
+                                 (1000, 127), (513, 2048)])
+def test_attention_online_tuned(o, d, M, N):
+    rng = np.random.default_rng(M * 7919 + N * 31 + d)
+    q, k, v = _problem(rng, M, N, d)
+    out = _gpu.poisoned((M, d))
+    kvq.attention_online(up(q), up(k), up(v), out)
+    torch.cuda.synchronize()
+    _close(down(out), o.attention_f32(q, k, v), f"M={M} N={N} d={d}")
+
+
+@pytest.mark.parametrize("d", [1, 17, 96, 256, 1024])
+def test_attention_online_generic_dims(o, d):
+    rng = np.random.default_rng(d)
+    M, N = 37, 301
+    q, k, v = _problem(rng, M, N, d)
+    out = _gpu.poisoned((M, d))
+    kvq.attention_online(up(q), up(k), up(v), out)
+    torch.cuda.synchronize()
+    _close(down(out), o.attention_f32(q, k, v), f"d={d}")
+
+
+@pytest.mark.parametrize("which", ["q", "k", "v", "out"])
+def test_attention_misaligned_takes_generic_path(o, which):
+    rng = np.random.default_rng(11)
+    M, N, d = 150, 333, 64
+    q, k, v = _problem(rng, M, N, d)
+    t = {"q": up(q), "k": up(k), "v": up(v), "out": _gpu.poisoned((M, d))}
+    base = torch.full((t[which].numel() + 1,), float("nan"), dtype=torch.float32, device="cuda")
+    shifted = base[1:].view(t[which].shape)
+    shifted.copy_(t[which])
+    t[which] = shifted
+    kvq.attention_online(t["q"], t["k"], t["v"], t["out"])
+    torch.cuda.synchronize()
+    _close(down(t["out"]), o.attention_f32(q, k, v), which)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 64, 1 << 20])
+def test_attention_split_requests(o, splits):
+    """Any split request (clamped to whole key tiles) gives the same result
+    within tolerance; the workspace is reused by a second, smaller problem."""
+    rng = np.random.default_rng(splits)
+    M, N, d = 300, 2500, 128
+    q, k, v = _problem(rng, M, N, d)
+    gq, gk, gv = up(q), up(k), up(v)
+    out = _gpu.poisoned((M, d))
+    p = kvq.attention_params(gq, gk, gv, out, num_splits=splits)
+    n = kvq.attention_workspace_size(p)
+    assert (n == 0) == (splits == 1)
+    ws = torch.full((max(n, 1),), 0xFF, dtype=torch.uint8, device="cuda")  # NaN bytes: records need no init
+    kvq.attention(gq, gk, gv, out, num_splits=splits, workspace=ws)
+    torch.cuda.synchronize()
+    _close(down(out), o.attention_f32(q, k, v), f"splits={splits}")
+    q2, k2, v2 = _problem(rng, 200, 1300, 128)
+    out2 = _gpu.poisoned((200, 128))
+    kvq.attention(up(q2), up(k2), up(v2), out2, num_splits=splits, workspace=ws)
+    torch.cuda.synchronize()
+    _close(down(out2), o.attention_f32(q2, k2, v2), f"second call, splits={splits}")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_attention_peaked_and_flat(o, d):
+    """Large logits (running max changes often, rescales taken) and identical
+    keys (uniform weights: the output is the mean of V)."""
+    rng = np.random.default_rng(d + 3)
+    M, N = 140, 1500
+    q, k, v = _problem(rng, M, N, d, qscale=8.0)
+    out = kvq.attention_online(up(q), up(k), up(v))
+    torch.cuda.synchronize()
+    _close(down(out), o.attention_f32(q, k, v), "peaked")
+    kf = np.repeat(rng.standard_normal((1, d)).astype(np.float32), N, axis=0)
+    out = kvq.attention_online(up(q), up(kf), up(v))
+    torch.cuda.synchronize()
+    _close(down(out), np.broadcast_to(v.astype(np.float64).mean(0), (M, d)), "flat")
+
+
+def test_attention_scale_and_side_stream(o):
+    rng = np.random.default_rng(5)
+    M, N, d = 130, 777, 128
+    q, k, v = _problem(rng, M, N, d)
+    s = torch.cuda.Stream()
+    gq, gk, gv = up(q), up(k), up(v)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        out = kvq.attention(gq, gk, gv, softmax_scale=0.25)
+        out_ref_abi = kvq.attention_online(gq, gk, gv)
+    s.synchronize()
+    # softmax(q k^T * 0.25) is the default-scale attention of q * 0.25 * sqrt(d).
+    _close(down(out), o.attention_f32(q * np.float32(0.25 * math.sqrt(d)), k, v), "scale 0.25")
+    _close(down(out_ref_abi), o.attention_f32(q, k, v), "side stream")
+
+
+def test_attention_prefill_size_sampled_rows():
+    """M = N = 4096, d = 128 (one prefill head): 96 sampled rows checked in
+    float64 on the CPU; the output is finite everywhere and each row lies in
+    the per-dim range of V (softmax weights are a convex combination)."""
+    M = N = 4096
+    d = 128
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    q = torch.randn((M, d), generator=gen, device="cuda")
+    k = torch.randn((N, d), generator=gen, device="cuda")
+    v = torch.randn((N, d), generator=gen, device="cuda")
+    out = kvq.attention_online(q, k, v)
+    torch.cuda.synchronize()
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(1))[:96]
+    qc, kc, vc = q.cpu().double(), k.cpu().double(), v.cpu().double()
+    s = (qc[rows] @ kc.T) / math.sqrt(d)
+    ref = torch.softmax(s, dim=1) @ vc
+    got = out.cpu()[rows].double()
+    assert torch.allclose(got, ref, atol=ATOL, rtol=RTOL), (got - ref).abs().max()
+    oc = out.cpu()
+    assert torch.isfinite(oc).all()
+    assert (oc <= vc.max(0).values.float() + 1e-5).all() and (oc >= vc.min(0).values.float() - 1e-5).all()

@@ -37,6 +37,8 @@ PLANTS = {
     7: "round half away from zero",
     8: "truncation",
     9: "value dequant drops v_scale",
+    10: "dense attention: 1/d instead of 1/sqrt(d)",
+    11: "dense attention: V transposed",
 }
 
 
