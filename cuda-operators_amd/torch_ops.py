@@ -18,6 +18,9 @@ allocates nothing once its workspace exists.
   torch.ops.kvq.prefill(k_new, v_new, k_cache, v_cache, k_scale, v_scale, start,
                         uniform_start, block_table) -> ()
       kvq_prefill_quantize_launch (fp32 or bf16 rows; mutates the caches).
+  torch.ops.kvq.attention(q, k, v, softmax_scale, num_splits) -> out
+      kvq_attention_launch: dense fp32 softmax(q k^T * scale) v, q [M, d],
+      k/v [N, d] (scale 0: 1/sqrt(d)).
 
 Workspaces are cached per (operator, device, stream) and grown on demand:
 launches on one stream are ordered, so they may share one; launches on
@@ -151,4 +154,22 @@ def _prefill_fake(k_new, v_new, k_cache, v_cache, k_scale, v_scale, start, unifo
     return None
 
 
-__all__ = ["decode", "paged_decode", "append", "prefill"]
+@torch.library.custom_op("kvq::attention", mutates_args=())
+def attention(q: Tensor, k: Tensor, v: Tensor, softmax_scale: float, num_splits: int) -> Tensor:
+    out = torch.empty_like(q)
+    p = kvq.attention_params(q, k, v, out, softmax_scale, num_splits)
+    stream = torch.cuda.current_stream(q.device)
+    nbytes = kvq.attention_workspace_size(p)  # 0: one split, or arguments the launch will reject
+    ws = _workspace(("attention", q.device.index, stream.cuda_stream), nbytes, q.device) if nbytes else None
+    code = kvq.lib().kvq_attention_launch(ctypes.byref(p), _opt(ws), nbytes, stream.cuda_stream)
+    if code != kvq.HIP_SUCCESS:
+        raise kvq.KvqError("kvq_attention_launch", code)
+    return out
+
+
+@attention.register_fake
+def _attention_fake(q, k, v, softmax_scale, num_splits):
+    return torch.empty_like(q)
+
+
+__all__ = ["decode", "paged_decode", "append", "prefill", "attention"]

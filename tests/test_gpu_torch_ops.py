@@ -123,3 +123,43 @@ def test_decode_graph_capture_replays(o, G):
         eager = torch.ops.kvq.decode(*args())
         torch.cuda.synchronize()
         assert np.array_equal(_bits(down(out)), _bits(down(eager))), f"replay {rep}"
+
+
+@pytest.mark.parametrize("M,N,splits", [(300, 2000, 0), (4096, 256, 0), (200, 1000, 5)])
+def test_attention_op_matches_c_abi(o, M, N, splits):
+    rng = np.random.default_rng(M + N)
+    d = 128
+    q, k, v = (rng.standard_normal(s).astype(np.float32) for s in ((M, d), (N, d), (N, d)))
+    g = [up(x) for x in (q, k, v)]
+    ref = kvq.attention(g[0], g[1], g[2], num_splits=splits)
+    out = torch.ops.kvq.attention(g[0], g[1], g[2], 0.0, splits)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(down(out)), _bits(down(ref)))
+    np.testing.assert_allclose(down(out), o.attention_f32(q, k, v), atol=1e-4, rtol=1e-3)
+    torch.library.opcheck(torch.ops.kvq.attention.default, (g[0], g[1], g[2], 0.0, splits),
+                          test_utils=("test_schema", "test_faketensor"))
+
+
+def test_attention_graph_capture_replays(o):
+    """Split attention (main + merge launches) captured once, replayed three
+    times with eager q updates between replays; each replay equals eager."""
+    rng = np.random.default_rng(9)
+    M, N, d = 256, 3000, 64
+    g = [up(rng.standard_normal(s).astype(np.float32)) for s in ((M, d), (N, d), (N, d))]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        torch.ops.kvq.attention(g[0], g[1], g[2], 0.0, 0)  # workspace exists before capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = torch.ops.kvq.attention(g[0], g[1], g[2], 0.0, 0)
+    for rep in range(3):
+        g[0].copy_(up(rng.standard_normal((M, d)).astype(np.float32)))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = torch.ops.kvq.attention(g[0], g[1], g[2], 0.0, 0)
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(down(out)), _bits(down(eager))), f"replay {rep}"

@@ -19,6 +19,7 @@ def test_ops_registered_with_mutation():
     assert _mutated(ops.paged_decode) == {"k_pages", "v_pages", "k_scale_pages", "v_scale_pages"}
     assert _mutated(ops.append) == {"k_cache", "v_cache", "k_scale", "v_scale"}
     assert _mutated(ops.prefill) == {"k_cache", "v_cache", "k_scale", "v_scale"}
+    assert _mutated(ops.attention) == set()
 
 
 def test_fake_shapes():
@@ -35,3 +36,6 @@ def test_fake_shapes():
         table = torch.empty(B, 3, dtype=torch.int32)
         out = torch.ops.kvq.paged_decode(q, pages, pages, ps, ps, table, lengths, 0, 0.0, 0, None, None)
         assert out.shape == q.shape and out.dtype == torch.float32
+        qa, ka = torch.empty(300, 64), torch.empty(1000, 64)
+        out = torch.ops.kvq.attention(qa, ka, ka, 0.0, 0)
+        assert out.shape == qa.shape and out.dtype == torch.float32
