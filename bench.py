@@ -134,7 +134,14 @@ def kernel_name(base, page):
     G = base.Hq // base.Hkv
     mfma = base.d == 128 and G % 4 == 0 and (page == 0 or (page & (page - 1) == 0 and page % 32 == 0))
     name = "decode_mfma" if mfma else "decode_fast"
-    return name + (" (+ schedule_kernel per step)" if not base.uniform else "")
+    if base.uniform:
+        return name
+    # Ragged: a matrix-core batch of <= 64 sequences that fits one round plans
+    # itself in the kernel; otherwise a schedule_kernel launch precedes it.
+    U = base.Hkv * (G // (8 if G % 8 == 0 else 4)) if mfma else 0
+    if mfma and base.B <= 64 and base.B <= 256 // U:
+        return name + " (split plan in-kernel)"
+    return name + " (+ schedule_kernel per step)"
 
 
 def main():

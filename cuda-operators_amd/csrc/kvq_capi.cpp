@@ -32,13 +32,21 @@ constexpr size_t kCounterBytes = 256 * 1024;
 constexpr long kMaxCounters = static_cast<long>(kCounterBytes / sizeof(int));
 // Workgroups a decode launch aims for when it picks the split count itself
 // (MI355X: 256 CUs).  An 8-wave VALU workgroup fills a CU's issue slots on its
-// own; two 4-wave MFMA workgroups share a CU.
+// own.  A 4-wave MFMA workgroup streams faster alone on a CU than two sharing
+// one (cfg3: 48.0 us at 256 workgroups, 52.0 us at 512, 62.3 us at 384), and
+// its split count rounds down so the grid stays within one round.
 constexpr int kTargetWorkgroupsValu = 256;
-constexpr int kTargetWorkgroupsMfma = 512;
+constexpr int kTargetWorkgroupsMfma = 256;
 // The same for the device split schedule of a ragged batch (work items of
 // equal size, so the target is the number of chunks over the whole batch).
 #ifndef KVQ_SCHED_TARGET_VALU
 #define KVQ_SCHED_TARGET_VALU 512
+#endif
+// Items per work unit of a ragged batch planned inside the matrix-core kernel
+// (one round): one 4-wave workgroup per CU streams faster than two (cfg2:
+// 36.7 us at 256, 38.5 us at 512, 47.8 us at 768).
+#ifndef KVQ_FIT_TARGET_MFMA
+#define KVQ_FIT_TARGET_MFMA 256
 #endif
 #ifndef KVQ_SCHED_TARGET_MFMA
 #define KVQ_SCHED_TARGET_MFMA 512
@@ -85,10 +93,28 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
     const long units = p.fast ? static_cast<long>(B) * Hkv * p.nsg : static_cast<long>(B) * Hq;
     const int gran = p.fast ? tile : 64;
     max_len = std::max(max_len, 1);
+    const int U = Hkv * p.nsg;
+    const int fit_items = KVQ_FIT_TARGET_MFMA / U;
+    if (ragged && requested == 0 && fused && p.kernel == kvq::Kernel::Mfma && units <= kMaxCounters &&
+        B <= kvq::kFitMaxSeqs && B <= fit_items && max_len <= (1 << 30)) {
+        // Small ragged batch on the matrix-core kernel: every workgroup plans
+        // the batch itself from the lengths (one round of at most fit_items
+        // items per work unit; no schedule launch).
+        p.fit = true;
+        p.counters = true;
+        p.sched_items = fit_items;
+        p.sched_gran = gran;
+        p.splits = 0;
+        p.chunk = 0;
+        const size_t recs = static_cast<size_t>(fit_items) * Hq;
+        p.counter_bytes = kCounterBytes;
+        p.ml_bytes = round_up(recs * 2 * sizeof(float), kAlign);
+        p.acc_bytes = round_up(recs * static_cast<size_t>(d) * sizeof(float), kAlign);
+        return p;
+    }
     if (ragged && requested == 0 && fused && p.fast && units <= kMaxCounters) {
         // Ragged batch: the split schedule is computed on the device from the
         // lengths.  Items (and records) <= B + target / units per sequence.
-        const int U = Hkv * p.nsg;
         p.scheduled = true;
         p.counters = true;
         p.sched_target = p.kernel == kvq::Kernel::Mfma ? KVQ_SCHED_TARGET_MFMA : KVQ_SCHED_TARGET_VALU;
@@ -98,7 +124,10 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
         p.chunk = 0;
         const size_t recs = static_cast<size_t>(p.sched_items) * Hq;
         p.counter_bytes = kCounterBytes;
-        p.sched_bytes = round_up((kvq::kSchedHeader + 2 * static_cast<size_t>(p.sched_items) + B) * sizeof(int), kAlign);
+        p.sched_bytes =
+            round_up((kvq::kSchedHeader + 2 * static_cast<size_t>(p.sched_items) + 2 * static_cast<size_t>(B)) *
+                         sizeof(int),
+                     kAlign);
         p.ml_bytes = round_up(recs * 2 * sizeof(float), kAlign);
         p.acc_bytes = round_up(recs * static_cast<size_t>(d) * sizeof(float), kAlign);
         return p;
@@ -115,8 +144,10 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
         // requested may run.
         if (p.fast && splits > 1) chunk = static_cast<int>(round_up(static_cast<size_t>(chunk), gran));
     } else {
-        const long target = p.kernel == kvq::Kernel::Mfma ? kTargetWorkgroupsMfma : kTargetWorkgroupsValu;
-        splits = (target + units - 1) / units;
+        if (p.kernel == kvq::Kernel::Mfma)
+            splits = std::max<long>(1, kTargetWorkgroupsMfma / units);
+        else
+            splits = (kTargetWorkgroupsValu + units - 1) / units;
         splits = std::min<long>(splits, (max_len + gran - 1) / gran);
         splits = std::max<long>(1, std::min<long>(splits, std::max(max_splits, 1)));
         chunk = static_cast<int>((max_len + splits - 1) / splits);
@@ -145,6 +176,8 @@ void bind_workspace(DecodeArgs& a, const DecodePlan& p, void* ws) {
     a.counters = p.counters ? reinterpret_cast<int*>(base) : nullptr;
     a.sched = p.scheduled ? reinterpret_cast<const int*>(base + p.counter_bytes) : nullptr;
     a.sched_items = p.sched_items;
+    a.fit_items = p.fit ? p.sched_items : 0;
+    a.fit_gran = p.sched_gran;
     const size_t ml = p.counter_bytes + p.sched_bytes;
     a.part_ml = p.ml_bytes ? reinterpret_cast<float*>(base + ml) : nullptr;
     a.part_acc = p.acc_bytes ? reinterpret_cast<float*>(base + ml + p.ml_bytes) : nullptr;

@@ -497,6 +497,7 @@ hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream) {
 
 long decode_grid(const DecodeArgs& a, const DecodePlan& p) {
     const long units = static_cast<long>(a.Hkv) * p.nsg;
+    if (p.fit) return units * p.sched_items;
     return p.scheduled ? units * p.sched_items : units * a.B * p.splits;
 }
 

@@ -79,7 +79,7 @@ __device__ __forceinline__ int pack_bytes(const int* b) {
            static_cast<int>(static_cast<unsigned>(b[3] & 0xff) << 24);
 }
 
-template <int G, bool PAGED>
+template <int G, bool PAGED, bool FIT>
 __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma(
     const DecodeArgs a) {
     static_assert(G == 4 || G == 8, "heads per workgroup");
@@ -102,7 +102,11 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     const int g = lane >> 4;   // 16-lane group
 
     SplitWork w;
-    if (!locate_work(a, w)) return;
+    if constexpr (FIT) {
+        if (!locate_fit(a, w)) return;
+    } else {
+        if (!locate_work(a, w)) return;
+    }
     const int unit = w.unit;
     const int bh = unit / a.nsg;
     const int sgi = unit - bh * a.nsg;
@@ -463,7 +467,11 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     __syncthreads();
 
     // Merge the waves and the hi/lo rows; one thread per (head, element).
-    const RecMap map = nsplit > 1 ? rec_map(a, b, bhq0) : RecMap{0, 0, 0};
+    RecMap map{0, 0, 0};
+    if (nsplit > 1) {
+        if constexpr (FIT) map = rec_map_fit(a, w, bhq0);
+        else map = rec_map(a, b, bhq0);
+    }
     for (int i = threadIdx.x; i < G * kMD; i += blockDim.x) {
         const int h = i / kMD;
         const int dim = i - h * kMD;
@@ -497,14 +505,26 @@ int mfma_heads_per_group(int G, int d) {
 hipError_t launch_decode_mfma(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(decode_grid(a, p)));
     const dim3 block(kMWaves * kWave);
+    const bool paged = a.pages.table != nullptr;
+    const bool fit = a.fit_items > 0;
     switch (p.sg) {
         case 4:
-            if (a.pages.table) hipLaunchKernelGGL((decode_mfma<4, true>), grid, block, 0, stream, a);
-            else hipLaunchKernelGGL((decode_mfma<4, false>), grid, block, 0, stream, a);
+            if (fit) {
+                if (paged) hipLaunchKernelGGL((decode_mfma<4, true, true>), grid, block, 0, stream, a);
+                else hipLaunchKernelGGL((decode_mfma<4, false, true>), grid, block, 0, stream, a);
+            } else {
+                if (paged) hipLaunchKernelGGL((decode_mfma<4, true, false>), grid, block, 0, stream, a);
+                else hipLaunchKernelGGL((decode_mfma<4, false, false>), grid, block, 0, stream, a);
+            }
             break;
         case 8:
-            if (a.pages.table) hipLaunchKernelGGL((decode_mfma<8, true>), grid, block, 0, stream, a);
-            else hipLaunchKernelGGL((decode_mfma<8, false>), grid, block, 0, stream, a);
+            if (fit) {
+                if (paged) hipLaunchKernelGGL((decode_mfma<8, true, true>), grid, block, 0, stream, a);
+                else hipLaunchKernelGGL((decode_mfma<8, false, true>), grid, block, 0, stream, a);
+            } else {
+                if (paged) hipLaunchKernelGGL((decode_mfma<8, true, false>), grid, block, 0, stream, a);
+                else hipLaunchKernelGGL((decode_mfma<8, false, false>), grid, block, 0, stream, a);
+            }
             break;
         default: return hipErrorInvalidValue;
     }

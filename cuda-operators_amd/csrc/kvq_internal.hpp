@@ -43,6 +43,8 @@ struct DecodeArgs {
     int* counters;           // [B * Hkv * nsg] arrival counters, or null (merge kernel)
     const int* sched;        // split schedule written by schedule_kernel, or null (static splits)
     int sched_items;         // capacity of the schedule's item list
+    int fit_items;           // > 0: the matrix-core kernel plans a ragged batch itself (locate_fit), this many items
+    int fit_gran;            // chunk granularity of that plan (tokens)
     PageMap pages;           // paged layout, or pages.table == null (contiguous rows of cap tokens)
     int B, Hq, Hkv, G, cap, d;
     int uniform_len;         // used when lengths == null
@@ -55,16 +57,20 @@ struct DecodeArgs {
 
 // Split schedule of a ragged batch, computed on the device from the lengths
 // by schedule_kernel before the decode launch (int words):
-//   [0] chunk: tokens per split;  [1] item count;  [2], [3] unused
+//   [0] chunk: the largest tokens per split;  [1] item count;  [2], [3] unused
 //   items  [kSchedHeader, + 2 * sched_items): (batch index, split index) per
-//          work item, every split of every sequence once: whole chunks first,
-//          then each sequence's last chunk, longest first (a length-0
+//          work item, every split of every sequence once (a length-0
 //          sequence has one empty item that writes its zero output);
-//   rec_base [B] after the items: the first partial record of sequence b; its
-//          split s owns records (rec_base[b] + s) * Hq + hq.
+//   seq [B] int2 after the items: (rec_base, chunk) of sequence b: its split
+//          s covers tokens [s * chunk, (s + 1) * chunk) and owns records
+//          (rec_base + s) * Hq + hq.
 // Workgroup i of the decode grid takes item i / U, work unit i % U of that
 // sequence (U = Hkv * nsg).
 constexpr int kSchedHeader = 4;
+
+// Most sequences of a ragged batch the matrix-core kernel plans itself (one
+// per lane of a wave).
+constexpr int kFitMaxSeqs = 64;
 
 // Which decode kernel a plan runs.
 enum class Kernel {
@@ -83,6 +89,7 @@ struct DecodePlan {
     int chunk;       // tokens per split
     bool counters;   // last-arriving split merges (fast path with a zeroed counter prefix)
     bool scheduled;  // ragged batch: the split schedule is computed on the device
+    bool fit;        // ragged batch planned inside the matrix-core kernel (one round, no schedule launch)
     int sched_items;     // schedule item capacity (scheduled)
     int sched_target;    // workgroups the schedule aims for (scheduled)
     int sched_gran;      // chunk granularity in tokens (scheduled)

@@ -5,17 +5,27 @@
 // length) leaves most workgroups of short sequences idle and the longest ones
 // finishing last.  One small workgroup instead reads the lengths and writes a
 // schedule (layout at kSchedHeader in kvq_internal.hpp) that the decode launch
-// right after it on the same stream follows:
+// right after it on the same stream follows.  `target` is the number of
+// workgroups the decode grid can run at once (S = target / units items):
 //
-// * chunk = total tokens x units per sequence / target workgroups, rounded up
-//   to the tile granularity and clamped to [gran, max_len rounded up]: about
-//   `target` equal chunks over the whole batch, whatever the length mix;
-// * whole chunks are dispatched first and each sequence's last (partial)
+// * one round (B <= S, every sequence can have its own items): the smallest
+//   chunk c (a multiple of the tile granularity) with
+//   sum_b ceil(len_b / c) <= S, so every item runs in the first round and the
+//   launch takes as long as its largest item.  The candidates lie in
+//   [total / S, total / (S - B)] (sum ceil(len / c) < total / c + B); one
+//   thread tests each.  Sequence b then splits into n_b = ceil(len_b / c)
+//   equal chunks of round_up(ceil(len_b / n_b), gran) <= c tokens, so its
+//   last split is not a small remainder.
+// * several rounds (B > S): chunk = total tokens x units / target, rounded
+//   up to the granularity: about `target` equal chunks over the whole batch.
+//   Whole chunks are dispatched first and each sequence's last (partial)
 //   chunk after them, longest first (64 size classes, a counting sort), so
 //   the work left at the end of the launch is small -- list scheduling in
-//   longest-processing-time order;
+//   longest-processing-time order.
 // * partial records are numbered per sequence (rec_base) so the workspace
 //   holds records only for splits that exist: at most B + target / units.
+#include <limits.h>
+
 #include "kvq_device.hpp"
 #include "kvq_internal.hpp"
 
@@ -65,28 +75,72 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
     __shared__ int s_tmp[kSchedWaves];
     __shared__ long long s_sum[kSchedWaves];
     __shared__ int s_class[kSizeClasses];
+    __shared__ int s_len[kSchedThreads];
+    __shared__ int s_best;
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
     const int wave = t / kWave;
 
     long long sum = 0;
-    for (int b = t; b < B; b += kSchedThreads) sum += clamped_len(lengths, b, max_len);
+    for (int b = t; b < B; b += kSchedThreads) {
+        const int len = clamped_len(lengths, b, max_len);
+        sum += len;
+        if (b < kSchedThreads) s_len[b] = len;
+    }
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
     if (lane == 0) s_sum[wave] = sum;
     if (t < kSizeClasses) s_class[t] = 0;
+    if (t == 0) s_best = INT_MAX;
     __syncthreads();
     long long total = 0;
 #pragma unroll
     for (int w = 0; w < kSchedWaves; w++) total += s_sum[w];
 
-    const long long want = (total * units + target - 1) / target;
+    int* items = sched + kSchedHeader;
+    int2* seq = reinterpret_cast<int2*>(items + 2 * items_cap);  // (rec_base, chunk) per sequence
     const long long cmax = (static_cast<long long>(max(max_len, 1)) + gran - 1) / gran * gran;
+    const int S = target / units;
+
+    if (B <= S && B <= kSchedThreads) {
+        // One round: the smallest chunk whose items all fit.
+        const long long lo = min(cmax, max(static_cast<long long>(gran), (total + S - 1) / S + gran - 1) / gran * gran);
+        const long long hi =
+            S > B ? max(lo, min(cmax, ((total + (S - B) - 1) / (S - B) + gran - 1) / gran * gran)) : cmax;
+        for (long long c = lo + static_cast<long long>(t) * gran; c <= hi; c += static_cast<long long>(kSchedThreads) * gran) {
+            long long n = 0;
+            for (int b = 0; b < B; b++) n += s_len[b] == 0 ? 1 : (s_len[b] + c - 1) / c;
+            if (n <= S || c == hi) atomicMin(&s_best, static_cast<int>(c));
+        }
+        __syncthreads();
+        const int chunk = s_best;
+        int n = 0, cb = gran;
+        if (t < B) {
+            const int len = s_len[t];
+            n = len == 0 ? 1 : (len + chunk - 1) / chunk;
+            cb = len == 0 ? gran : ((len + n - 1) / n + gran - 1) / gran * gran;
+        }
+        int tot = 0;
+        const int pre = block_exclusive_scan(n, s_tmp, &tot);
+        if (t < B) {
+            seq[t] = make_int2(pre, cb);
+            for (int s = 0; s < n; s++) {
+                if (pre + s < items_cap) {
+                    items[2 * (pre + s)] = t;
+                    items[2 * (pre + s) + 1] = s;
+                }
+            }
+        }
+        if (t == 0) {
+            sched[0] = chunk;
+            sched[1] = min(tot, items_cap);
+        }
+        return;
+    }
+
+    const long long want = (total * units + target - 1) / target;
     const long long c = (want + gran - 1) / gran * gran;
     const int chunk = static_cast<int>(min(cmax, max(static_cast<long long>(gran), c)));
-
-    int* items = sched + kSchedHeader;
-    int* rec_base = items + 2 * items_cap;
     int rec_carry = 0, full_carry = 0;
     for (int b0 = 0; b0 < B; b0 += kSchedThreads) {
         const int b = b0 + t;
@@ -100,7 +154,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
         const int pre_n = block_exclusive_scan(n, s_tmp, &tot_n);
         const int pre_f = block_exclusive_scan(full, s_tmp, &tot_f);
         if (b < B) {
-            rec_base[b] = rec_carry + pre_n;
+            seq[b] = make_int2(rec_carry + pre_n, chunk);
             for (int s = 0; s < full; s++) {
                 const int pos = full_carry + pre_f + s;
                 if (pos < items_cap) {

@@ -3,6 +3,7 @@
 // last-arrival handshake.
 #pragma once
 
+#include <limits.h>
 #include <math.h>
 
 #include "kvq_device.hpp"
@@ -21,6 +22,7 @@ __device__ __forceinline__ int seq_len_of(const DecodeArgs& a, int b) {
 // t0 = t1 = 0 (its workgroup writes the zero output).
 struct SplitWork {
     int unit, b, split, nsplit, len, t0, t1;
+    int rec;  // in-kernel plan: the sequence's first partial record (see locate_fit)
 };
 
 // Work of workgroup blockIdx.x, from the static split grid (split-major:
@@ -32,10 +34,10 @@ __device__ __forceinline__ bool locate_work(const DecodeArgs& a, SplitWork& w) {
     if (a.sched) {
         const int item = blockIdx.x / U;
         if (item >= a.sched[1]) return false;
-        chunk = a.sched[0];
         w.b = a.sched[kSchedHeader + 2 * item];
         w.split = a.sched[kSchedHeader + 2 * item + 1];
         w.unit = w.b * U + (blockIdx.x - item * U);
+        chunk = a.sched[kSchedHeader + 2 * a.sched_items + 2 * w.b + 1];
     } else {
         const int units = a.B * U;
         w.split = blockIdx.x / units;
@@ -51,6 +53,80 @@ __device__ __forceinline__ bool locate_work(const DecodeArgs& a, SplitWork& w) {
     return true;
 }
 
+// In-kernel one-round split plan of a ragged batch (a.fit_items > 0; at most
+// kFitMaxSeqs sequences, one per lane).  The decode grid has fit_items x U
+// workgroups.  Each wave derives the same plan from the device lengths with
+// lane operations only, so it needs no LDS, no barrier and no separate
+// schedule launch:
+// * chunk = the smallest multiple c of the tile granularity with
+//   sum_b max(1, ceil(len_b / c)) <= fit_items, i.e. every item runs in the
+//   first round and the launch takes as long as its largest item.  Lanes test
+//   64 candidates at a time between total / S and total / (S - B) (the sum is
+//   below total / c + B, so the upper end always fits), narrowing until the
+//   candidates are one granule apart.
+// * sequence b splits into n_b = max(1, ceil(len_b / c)) equal chunks of
+//   round_up(ceil(len_b / n_b), gran) <= c tokens (its last split is not a
+//   small remainder); items are numbered sequence by sequence, and the items
+//   before sequence b are also its first partial record (rec).
+__device__ __forceinline__ int fit_items_for(int len_sgpr, int c) {
+    return len_sgpr == 0 ? 1 : static_cast<int>((static_cast<unsigned>(len_sgpr) + c - 1) / static_cast<unsigned>(c));
+}
+
+__device__ inline bool locate_fit(const DecodeArgs& a, SplitWork& w) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int B = a.B;
+    const int S = a.fit_items;
+    const int gran = a.fit_gran;
+    const int len = lane < B ? seq_len_of(a, lane) : 0;
+    long long total = len;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) total += __shfl_xor(total, off);
+    auto round_g = [&](long long x) { return (x + gran - 1) / gran * gran; };
+    auto clamp_ll = [](long long x, long long l, long long h) { return x < l ? l : (x > h ? h : x); };
+    const int cmax = static_cast<int>(round_g(max(a.max_len, 1)));
+    const int lo0 = static_cast<int>(clamp_ll(round_g((total + S - 1) / S), gran, cmax));
+    int lo = lo0;
+    int hi = S > B ? static_cast<int>(clamp_ll(round_g((total + (S - B) - 1) / (S - B)), lo0, cmax)) : cmax;
+    int chunk = hi;
+    for (;;) {
+        const int step = max(gran, static_cast<int>(round_g((hi - lo + kWave - 2) / (kWave - 1))));
+        const int c = min(hi, lo + lane * step);
+        int n = 0;
+        for (int j = 0; j < B; j++) n += fit_items_for(__builtin_amdgcn_readlane(len, j), c);
+        int best = n <= S ? c : INT_MAX;
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) best = min(best, __shfl_xor(best, off));
+        chunk = best;  // hi always fits
+        if (step == gran) break;
+        lo = max(lo, best - step + gran);
+        hi = best;
+    }
+    const int nb = lane < B ? fit_items_for(len, chunk) : 0;
+    const int cb = lane < B && len > 0 ? static_cast<int>(round_g((len + nb - 1) / nb)) : gran;
+    int incl = nb;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int y = __shfl_up(incl, off);
+        if (lane >= off) incl += y;
+    }
+    const int count = __builtin_amdgcn_readlane(incl, kWave - 1);
+    const int U = a.Hkv * a.nsg;
+    const int item = blockIdx.x / U;
+    if (item >= count) return false;
+    const int excl = incl - nb;
+    const int b = __builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < B && excl <= item)) - 1;
+    w.b = b;
+    w.rec = __builtin_amdgcn_readlane(excl, b);
+    w.split = item - w.rec;
+    w.unit = b * U + (blockIdx.x - item * U);
+    w.len = __builtin_amdgcn_readlane(len, b);
+    w.nsplit = __builtin_amdgcn_readlane(nb, b);
+    const int cs = __builtin_amdgcn_readlane(cb, b);
+    w.t0 = w.split * cs;
+    w.t1 = min(w.len, w.t0 + cs);
+    return true;
+}
+
 // Partial record of row bhq0 + h, split s: r0 + h * hs + s * ss (records of
 // 2 floats in part_ml, d floats in part_acc).
 struct RecMap {
@@ -59,11 +135,18 @@ struct RecMap {
 };
 
 __device__ __forceinline__ RecMap rec_map(const DecodeArgs& a, int b, size_t bhq0) {
+    if (a.fit_items > 0) return {0, 0, 0};  // callers under an in-kernel plan use rec_map_fit
     if (a.sched) {
-        const int base = a.sched[kSchedHeader + 2 * a.sched_items + b];
+        const int base = a.sched[kSchedHeader + 2 * a.sched_items + 2 * b];
         return {static_cast<size_t>(base) * a.Hq + (bhq0 - static_cast<size_t>(b) * a.Hq), 1, a.Hq};
     }
     return {bhq0 * a.splits, a.splits, 1};
+}
+
+// Records of an in-kernel plan (locate_fit): sequence b's split s owns
+// records (rec + s) * Hq + hq.
+__device__ __forceinline__ RecMap rec_map_fit(const DecodeArgs& a, const SplitWork& w, size_t bhq0) {
+    return {static_cast<size_t>(w.rec) * a.Hq + (bhq0 - static_cast<size_t>(w.b) * a.Hq), 1, a.Hq};
 }
 
 // U consecutive per-token scales (U in {1,2,4,8}); p is U*4-byte aligned when

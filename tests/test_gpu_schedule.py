@@ -105,3 +105,65 @@ def test_schedule_repeated_launches_new_lengths(o, G):
         torch.cuda.synchronize()
         want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
         assert_close(down(out), want, what=f"launch {it}")
+
+
+@pytest.mark.parametrize("G", [1, 4])
+def test_schedule_all_empty(o, G):
+    """Every length 0 (no tokens at all): one empty item per sequence, zero output rows."""
+    rng = np.random.default_rng(7 + G)
+    B, Hkv, cap, d = 5, 2, 256, 128
+    lengths = np.zeros(B, np.int32)
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, lengths=lengths)
+    got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)[0]
+    assert np.array_equal(got, np.zeros_like(got))
+
+
+@pytest.mark.parametrize("B", [255, 256, 257])
+def test_schedule_at_the_one_round_limit(o, B):
+    """Matrix-core kernel, G = 8, Hkv = 2: the schedule runs everything in one
+    round while B <= 512 / 2 sequences, and switches to longest-first rounds
+    above that; both sides of the switch are exact."""
+    rng = np.random.default_rng(B)
+    Hkv, G, cap, d = 2, 8, 640, 128
+    lengths = rng.integers(0, cap + 1, B).astype(np.int32)
+    lengths[:3] = [cap, 0, 1]
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, lengths=lengths)
+    got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)[0]
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert_close(got, want, what=f"B={B}")
+
+
+@pytest.mark.parametrize("B", [63, 64, 65])
+@pytest.mark.parametrize("append", [False, True])
+def test_in_kernel_plan_limit(o, B, append):
+    """Matrix-core kernel, Hkv = 4, G = 4: a ragged batch of up to 64
+    sequences is planned inside the decode kernel (256 / 4 = 64 items per kv
+    head, so B = 64 leaves one item per sequence); B = 65 goes back to the
+    schedule launch.  Lengths include 0, 1 and the capacity."""
+    rng = np.random.default_rng(B + 100 * append)
+    Hkv, G, cap, d = 4, 4, 520, 128
+    lengths = rng.integers(0, cap + 1, B).astype(np.int32)
+    lengths[:4] = [cap, 0, 1, 129]
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, lengths=lengths)
+    kn = vn = None
+    if append:
+        kn = rng.standard_normal((B, Hkv, d)).astype(np.float32)
+        vn = rng.standard_normal((B, Hkv, d)).astype(np.float32)
+    got, gk, _, gks, _ = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths, k_new=kn, v_new=vn)
+    if append:
+        o.append(kn, vn, p["k"], p["v"], p["ks"], p["vs"], positions=lengths - 1)
+        assert np.array_equal(gk, p["k"]) and np.array_equal(_bits(gks), _bits(p["ks"]))
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert_close(got, want, what=f"B={B} append={append}")
+
+
+def test_in_kernel_plan_one_long_sequence(o):
+    """A few sequences, one much longer: the in-kernel plan cuts the long one
+    into many equal splits (more than one narrowing round of the chunk search)."""
+    rng = np.random.default_rng(12)
+    B, Hkv, G, cap, d = 6, 2, 8, 70000, 128
+    lengths = np.array([70000, 3, 0, 640, 129, 5000], np.int32)
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, lengths=lengths)
+    got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)[0]
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert_close(got, want, what="one long")
