@@ -123,9 +123,9 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const Pre
             for (int i = 0; i < EPL; i++) am = fmaxf(am, fabsf(e[i]));
             const float scale = quant_scale(lanes_max<LPR>(am));
             if (row >= a.rows) continue;
-            const unsigned bh = row / a.L;
+            const unsigned bh = fastdiv(row, a.divL);
             const int t = static_cast<int>(row - bh * a.L);
-            const int b = static_cast<int>(bh / a.Hkv);
+            const int b = static_cast<int>(fastdiv(bh, a.divH));
             const int h = static_cast<int>(bh - static_cast<unsigned>(b) * a.Hkv);
             const int pos = (a.start ? a.start[b] : a.uniform_start) + t;
             if (pos < 0 || pos >= a.cap) continue;
@@ -155,9 +155,9 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_generic_kernel(c
     const unsigned step = gridDim.x * kPrefillWaves;
     for (unsigned row = blockIdx.x * kPrefillWaves + threadIdx.x / kWave; row < a.rows; row += step) {
         const void* xr = x + static_cast<size_t>(row) * d * (BF16 ? 2 : 4);
-        const unsigned bh = row / a.L;
+        const unsigned bh = fastdiv(row, a.divL);
         const int t = static_cast<int>(row - bh * a.L);
-        const int b = static_cast<int>(bh / a.Hkv);
+        const int b = static_cast<int>(fastdiv(bh, a.divH));
         const int h = static_cast<int>(bh - static_cast<unsigned>(b) * a.Hkv);
         const int pos = (a.start ? a.start[b] : a.uniform_start) + t;
         if (pos < 0 || pos >= a.cap) continue;

@@ -554,6 +554,8 @@ hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, 
         a.ks = a.vs = scale;
         a.Hkv = 1;
         a.L = static_cast<int>(rows);
+        a.divL = kvq::make_fastdiv(static_cast<uint32_t>(std::max<int64_t>(rows, 1)));
+        a.divH = kvq::make_fastdiv(1);
         a.cap = static_cast<int>(rows);
         a.rows = static_cast<unsigned>(rows);
         a.planes = 1;
@@ -648,6 +650,8 @@ hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t 
     a.uniform_start = p->uniform_start;
     a.Hkv = p->num_kv_heads;
     a.L = p->tokens;
+    a.divL = kvq::make_fastdiv(static_cast<uint32_t>(std::max(p->tokens, 1)));
+    a.divH = kvq::make_fastdiv(static_cast<uint32_t>(p->num_kv_heads));
     a.rows = static_cast<unsigned>(rows);
     a.planes = 2;
     const bool vec_ok = aligned16(p->k_new) && aligned16(p->v_new) &&

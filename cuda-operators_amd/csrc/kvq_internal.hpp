@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "kvq_fastdiv.hpp"
+
 namespace kvq {
 
 // Paged cache: k/v are page pools [num_pages, Hkv, size, d], their scales
@@ -128,6 +130,7 @@ struct PrefillArgs {
     const int32_t* start;
     int uniform_start;
     int Hkv, L, cap;
+    FastDiv divL, divH;  // division of row indices by L and Hkv
     unsigned rows;
     int planes;  // 2: K and V; 1: K only
     PageMap pages;

@@ -251,3 +251,44 @@ def test_attention_workspace_plan(L):
     assert size(128, 64, 128) == 0  # one key tile: nothing to split
     # A requested split count is clamped to whole key tiles.
     assert size(128, 8192, 64, splits=1 << 20) == size(128, 8192, 64, splits=8192 // 64) > 0
+
+
+def test_fastdiv_matches_division(tmp_path):
+    """kvq_fastdiv.hpp (division by a launch-invariant divisor as a multiply
+    and shifts) equals integer division: every divisor up to 4096 against
+    edge and random numerators, powers of two and their neighbours up to
+    2^31, and random large divisors; built from the same header with g++."""
+    src = tmp_path / "fastdiv.cpp"
+    src.write_text(r'''
+#include <stdio.h>
+#include <stdint.h>
+#include <random>
+#include "kvq_fastdiv.hpp"
+static int check(uint32_t d, uint32_t n) {
+    const kvq::FastDiv f = kvq::make_fastdiv(d);
+    if (kvq::fastdiv(n, f) != n / d) { printf("FAIL d=%u n=%u got %u\n", d, n, kvq::fastdiv(n, f)); return 1; }
+    return 0;
+}
+int main() {
+    std::mt19937_64 rng(7);
+    int bad = 0;
+    auto edge = [&](uint32_t d) {
+        const uint32_t ns[] = {0u, 1u, d - 1, d, d + 1, 2 * d - 1, 2 * d, 0x7fffffffu, 0x80000000u, 0xfffffffeu,
+                               0xffffffffu, 0xffffffffu - 0xffffffffu % d, 0xffffffffu - 0xffffffffu % d - 1};
+        for (uint32_t n : ns) bad += check(d, n);
+        for (int i = 0; i < 64; i++) bad += check(d, static_cast<uint32_t>(rng()));
+    };
+    for (uint32_t d = 1; d <= 4096; d++) edge(d);
+    for (int l = 1; l < 31; l++)
+        for (int o = -1; o <= 1; o++) edge((1u << l) + o);
+    edge(0x7fffffffu);
+    for (int i = 0; i < 2000; i++) edge(1 + static_cast<uint32_t>(rng() % 0x7fffffffu));
+    printf("%s\n", bad ? "FAILED" : "OK");
+    return bad != 0;
+}
+''')
+    exe = tmp_path / "fastdiv"
+    csrc = os.path.join(REPO, "cuda-operators_amd", "csrc")
+    subprocess.run(["g++", "-std=c++17", "-O2", "-I", csrc, str(src), "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.strip().endswith("OK"), r.stdout[-2000:]

@@ -69,6 +69,53 @@ def test_quantize_golden_fixture():
     assert np.array_equal(down(gq), g["q"]) and np.array_equal(_bits(down(gs)), _bits(g["scale"]))
 
 
+def near_tie_rows(rng, d, rows):
+    """Rows whose elements sit at, and one or two ulps either side of, the
+    rounding boundaries (k + 1/2) * scale of their own scale: element 0 sets
+    amax, so scale = fl(amax / 127); the rest are fl((k + 1/2) * scale) moved
+    by -2..2 ulps, for k across the int8 range, at varied magnitudes.  These
+    are the elements whose product with 1/scale can round differently from
+    the IEEE quotient."""
+    out = np.empty((rows, d), np.float32)
+    for r in range(rows):
+        amax = np.float32(np.exp(rng.uniform(-30.0, 30.0)))
+        scale = np.float32(amax / np.float32(127.0))
+        k = rng.integers(-127, 127, d - 1).astype(np.float32)
+        x = ((k + np.float32(0.5)) * scale).astype(np.float32)
+        for _ in range(2):
+            step = rng.integers(-1, 2, d - 1)
+            x = np.where(step > 0, np.nextafter(x, np.float32(np.inf)),
+                         np.where(step < 0, np.nextafter(x, np.float32(-np.inf)), x)).astype(np.float32)
+        x = np.clip(x, -amax, amax)
+        out[r, 0] = amax if r % 2 == 0 else -amax
+        out[r, 1:] = x
+    return out
+
+
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
+def test_quantize_near_ties_bit_exact(d):
+    """The quantiser's multiply-by-reciprocal path must give the IEEE
+    division's integers on elements next to rounding boundaries (the oracle
+    divides), fp32 and bf16 inputs, through the prefill kernel."""
+    o = orc.get()
+    rng = np.random.default_rng(100 + d)
+    x = near_tie_rows(rng, d, 2048)
+    gq, gs = kvq.quantize_rows(up(x))
+    torch.cuda.synchronize()
+    wq, ws = o.quantize_rows(x)
+    assert np.array_equal(_bits(down(gs)), _bits(ws))
+    diff = np.argwhere(down(gq) != wq)
+    assert diff.size == 0, f"{len(diff)} elements differ, first {diff[:5].tolist()}"
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    xbf = xb.to(torch.float32).numpy()
+    k = torch.zeros((1, 1, x.shape[0], d), dtype=torch.int8, device="cuda")
+    ks = torch.zeros((1, 1, x.shape[0]), dtype=torch.float32, device="cuda")
+    kvq.prefill(xb.view(1, 1, -1, d).cuda(), xb.view(1, 1, -1, d).cuda(), k, k.clone(), ks, ks.clone())
+    torch.cuda.synchronize()
+    bq, bs = o.quantize_rows(xbf)
+    assert np.array_equal(down(k)[0, 0], bq) and np.array_equal(_bits(down(ks)[0, 0]), _bits(bs))
+
+
 def test_quantize_many_rows():
     """A bulk prefill-sized tensor (grid-stride path) stays bit-exact."""
     o = orc.get()
