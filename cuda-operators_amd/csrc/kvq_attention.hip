@@ -4,7 +4,8 @@
 //
 // attention_mfma<D> (d in {32, 64, 128}): a workgroup of 8 waves owns 128
 // queries (16 per wave) and one split of the keys, which it streams through
-// LDS in 64-key tiles shared by all its waves.  Both products run on
+// LDS in 64-key tiles shared by all its waves (two LDS buffers: one barrier
+// per tile; 135 KB of LDS at d = 128).  Both products run on
 // v_mfma_f32_16x16x4_f32 (fp32 in, fp32 accumulate: the same arithmetic as
 // fp32 FMAs, in another order):
 //   * S^T = K Q^T per 16-key block: A = K rows from LDS, B = this wave's q
@@ -108,9 +109,8 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
     constexpr int KS = D + 4;   // LDS row stride in floats (16-byte pad: conflict-free row reads)
     constexpr int NL = kAK * D / 4 / (kAWaves * kWave);  // float4 per thread per tile per tensor
     static_assert(NL >= 1, "tile load shape");
-    __shared__ __align__(16) float s_kv[2 * kAK * KS];  // K tile, V tile
-    float* const s_k = s_kv;
-    float* const s_v = s_kv + kAK * KS;
+    __shared__ __align__(16) float s_kv[2][2 * kAK * KS];  // two (K tile, V tile) buffers
+    int cur = 0;
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -158,7 +158,9 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
             pv[j] = make_float4(y.x * keep, y.y * keep, y.z * keep, y.w * keep);
         }
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](int buf) {
+        float* const s_k = s_kv[buf];
+        float* const s_v = s_kv[buf] + kAK * KS;
 #pragma unroll
         for (int j = 0; j < NL; j++) {
             const int f = threadIdx.x + j * kAWaves * kWave;
@@ -169,12 +171,17 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
         }
     };
 
-    if (k0 < k1) load_tile(k0);
-    for (int t0 = k0; t0 < k1; t0 += kAK) {
-        __syncthreads();  // every wave is done with the previous tile
-        store_tile();
+    // Tile t is computed from LDS buffer t % 2 while tile t + 1 waits in
+    // registers (loaded during tile t - 1) and tile t + 2 is loading.
+    if (k0 < k1) {
+        load_tile(k0);
+        store_tile(0);
+        if (k0 + kAK < k1) load_tile(k0 + kAK);
         __syncthreads();
-        if (t0 + kAK < k1) load_tile(t0 + kAK);  // the next tile is in flight during compute
+    }
+    for (int t0 = k0; t0 < k1; t0 += kAK) {
+        const float* const s_k = s_kv[cur];
+        const float* const s_v = s_kv[cur] + kAK * KS;
 
         // S^T for the 4 key blocks: sv[4 kb + i] = score of key t0 + 16 kb + 4 g + i, query r.
         float sv[16];
@@ -241,6 +248,15 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
                     o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[c], sv[4 * kb + i], o[c], 0, 0, 0);
             }
         }
+        // The next tile (in registers since the previous iteration) goes to the
+        // idle buffer, which every wave finished reading before the last
+        // barrier; the tile after it starts loading.  One barrier per tile.
+        if (t0 + kAK < k1) {
+            store_tile(cur ^ 1);
+            if (t0 + 2 * kAK < k1) load_tile(t0 + 2 * kAK);
+        }
+        __syncthreads();
+        cur ^= 1;
     }
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
