@@ -57,7 +57,9 @@ def parse():
     ap.add_argument("--replicas", type=int, default=0, help="cache replicas (0 = enough for 512 MiB, >= 3)")
     ap.add_argument("--page-size", type=int, default=0,
                     help="run the same step through a paged cache with this many tokens per page "
-                         "(pages scattered in a shuffled pool; 0 = contiguous cache)")
+                         "(0 = contiguous cache)")
+    ap.add_argument("--page-order", choices=("shuffled", "sequential"), default="shuffled",
+                    help="paged cache: pages scattered in a shuffled pool, or in sequence order")
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="max seconds for the CPU baseline")
@@ -103,15 +105,16 @@ def cpu_baseline(prob, budget_s):
     }
 
 
-def paged_decoder(kvq, p, out, page, splits, seed):
-    """The problem's cache moved into a pool of `page`-token pages in shuffled
-    order (block table = the shuffle), wrapped in a PagedDecoder."""
+def paged_decoder(kvq, p, out, page, splits, seed, order="shuffled"):
+    """The problem's cache moved into a pool of `page`-token pages, in shuffled
+    order (block table = the shuffle) or in sequence order, wrapped in a
+    PagedDecoder."""
     import torch
 
     B, Hkv, cap, d = p.k.shape
     npg = -(-cap // page)
     gen = torch.Generator().manual_seed(seed)
-    perm = torch.randperm(B * npg, generator=gen).to(p.k.device)
+    perm = (torch.randperm(B * npg, generator=gen) if order == "shuffled" else torch.arange(B * npg)).to(p.k.device)
 
     def pool(x):  # [B, Hkv, cap, ...] -> [B * npg, Hkv, page, ...] in perm order
         pad = torch.zeros((B, Hkv, npg * page) + tuple(x.shape[3:]), dtype=x.dtype, device=x.device)
@@ -173,7 +176,7 @@ def main():
         reps.append(c)
     outs = [torch.empty_like(base.q) for _ in reps]
     if args.page_size > 0:
-        decs = [paged_decoder(kvq, p, o, args.page_size, args.splits, args.seed + i)
+        decs = [paged_decoder(kvq, p, o, args.page_size, args.splits, args.seed + i, args.page_order)
                 for i, (p, o) in enumerate(zip(reps, outs))]
     else:
         decs = [kvq.Decoder(p.q, p.k, p.v, p.ks, p.vs, o, lengths=p.lengths,
@@ -273,7 +276,8 @@ def main():
             "kv_bytes_per_step": kv_bytes,
             "replicas": R,
             "splits": decs[0].params.num_splits or "auto",
-            "layout": f"paged, {args.page_size} tokens per page" if args.page_size > 0 else "contiguous",
+            "layout": (f"paged, {args.page_size} tokens per page, {args.page_order} pool" if args.page_size > 0
+                       else "contiguous"),
             "parallelism": "single GPU",
         },
         "roofline": {
