@@ -275,9 +275,13 @@ typedef struct kvq_attention_params {
 size_t kvq_attention_workspace_size(const kvq_attention_params* p);
 
 /* attention_online_launch with an explicit scale, split request and
- * caller-owned workspace; allocates nothing.  With splits, a second kernel
- * merges the records.  Launches that share a workspace must be ordered (one
- * stream). */
+ * caller-owned workspace (16-byte aligned, at least
+ * kvq_attention_workspace_size(p) bytes); allocates nothing.  With splits, a
+ * second kernel merges the records.  Launches that share a workspace must be
+ * ordered (one stream).  hipErrorInvalidValue, before any HIP call, for the
+ * checks of attention_online_launch, M or N above INT_MAX - 1024, a negative
+ * num_splits, or a workspace too small, NULL or misaligned when one is
+ * needed. */
 hipError_t kvq_attention_launch(const kvq_attention_params* p, void* workspace, size_t workspace_bytes,
                                 hipStream_t stream);
 
