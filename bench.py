@@ -52,7 +52,7 @@ def parse():
                     help="after the warm-up steps, keep launching untimed steps until this much wall "
                          "time has passed since the warm-up began (MI355X runs this kernel ~15%% slower "
                          "during its first ~20 ms of sustained load than in steady state)")
-    ap.add_argument("--config", default="cfg1", help="cfg0..cfg4 (default cfg1, the headline)")
+    ap.add_argument("--config", default="cfg1", help="cfg0..cfg4 (default cfg1, the headline); cfg2m: cfg2's lengths with MHA")
     ap.add_argument("--splits", type=int, default=0, help="splits per sequence (0 = library choice)")
     ap.add_argument("--replicas", type=int, default=0, help="cache replicas (0 = enough for 512 MiB, >= 3)")
     ap.add_argument("--page-size", type=int, default=0,
@@ -139,10 +139,15 @@ def kernel_name(base, page):
     name = "decode_mfma" if mfma else "decode_fast"
     if base.uniform:
         return name
-    # Ragged: a matrix-core batch of <= 64 sequences that fits one round plans
-    # itself in the kernel; otherwise a schedule_kernel launch precedes it.
-    U = base.Hkv * (G // (8 if G % 8 == 0 else 4)) if mfma else 0
-    if mfma and base.B <= 64 and base.B <= 256 // U:
+    # Ragged: a batch of <= 64 sequences that fits one round plans itself in
+    # the kernel (matrix-core kernel, or the FMA kernel with <= 2 query heads
+    # per kv head); otherwise a schedule_kernel launch precedes it.
+    if mfma:
+        U, slots = base.Hkv * (G // (8 if G % 8 == 0 else 4)), 256
+    else:
+        sg = 4 if G % 4 == 0 else (2 if G % 2 == 0 else 1)
+        U, slots = (base.Hkv * (G // sg) if sg <= 2 else 0), 512
+    if U and base.B <= 64 and base.B <= slots // U:
         return name + " (split plan in-kernel)"
     return name + " (+ schedule_kernel per step)"
 

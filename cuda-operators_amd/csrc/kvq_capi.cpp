@@ -45,6 +45,11 @@ constexpr int kTargetWorkgroupsMfma = 256;
 // Items per work unit of a ragged batch planned inside the matrix-core kernel
 // (one round): one 4-wave workgroup per CU streams faster than two (cfg2:
 // 36.7 us at 256, 38.5 us at 512, 47.8 us at 768).
+// The same for the 8-wave FMA kernel, two of which share a CU (a ragged
+// B8 H32 d128 MHA batch: 59.8 us, against 63.7 us with the schedule launch).
+#ifndef KVQ_FIT_TARGET_VALU
+#define KVQ_FIT_TARGET_VALU 512
+#endif
 #ifndef KVQ_FIT_TARGET_MFMA
 #define KVQ_FIT_TARGET_MFMA 256
 #endif
@@ -94,12 +99,13 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
     const int gran = p.fast ? tile : 64;
     max_len = std::max(max_len, 1);
     const int U = Hkv * p.nsg;
-    const int fit_items = KVQ_FIT_TARGET_MFMA / U;
-    if (ragged && requested == 0 && fused && p.kernel == kvq::Kernel::Mfma && units <= kMaxCounters &&
-        B <= kvq::kFitMaxSeqs && B <= fit_items && max_len <= (1 << 30)) {
-        // Small ragged batch on the matrix-core kernel: every workgroup plans
-        // the batch itself from the lengths (one round of at most fit_items
-        // items per work unit; no schedule launch).
+    const bool fit_kernel = p.kernel == kvq::Kernel::Mfma || (p.kernel == kvq::Kernel::Valu && p.sg <= 2);
+    const int fit_items = (p.kernel == kvq::Kernel::Mfma ? KVQ_FIT_TARGET_MFMA : KVQ_FIT_TARGET_VALU) / U;
+    if (ragged && requested == 0 && fused && fit_kernel && units <= kMaxCounters && B <= kvq::kFitMaxSeqs &&
+        B <= fit_items && max_len <= (1 << 30)) {
+        // Small ragged batch: every workgroup plans the batch itself from the
+        // lengths (one round of at most fit_items items per work unit; no
+        // schedule launch).
         p.fit = true;
         p.counters = true;
         p.sched_items = fit_items;

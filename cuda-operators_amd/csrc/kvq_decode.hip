@@ -114,7 +114,7 @@ __device__ __forceinline__ void attend(const float (&qr)[SG][16], const int4 (&k
     }
 }
 
-template <int D, int SG, bool PAGED>
+template <int D, int SG, bool PAGED, bool FIT>
 __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArgs a) {
     using Geo = FastGeom<D, SG>;
     constexpr int LPT = Geo::LPT;
@@ -131,7 +131,11 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     const int ds = lane % LPT;  // 16-element slice of the head dim
 
     SplitWork w;
-    if (!locate_work(a, w)) return;
+    if constexpr (FIT) {
+        if (!locate_fit(a, w)) return;
+    } else {
+        if (!locate_work(a, w)) return;
+    }
     const int unit = w.unit;
     const int bh = unit / a.nsg;
     const int sgi = unit - bh * a.nsg;
@@ -351,7 +355,11 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     __syncthreads();
 
     // Merge the waves; one thread per (head, element).
-    const RecMap map = nsplit > 1 ? rec_map(a, b, bhq0) : RecMap{0, 0, 0};
+    RecMap map{0, 0, 0};
+    if (nsplit > 1) {
+        if constexpr (FIT) map = rec_map_fit(a, w, bhq0);
+        else map = rec_map(a, b, bhq0);
+    }
     for (int i = threadIdx.x; i < SG * D; i += blockDim.x) {
         const int h = i / D;
         const int dim = i - h * D;
@@ -443,8 +451,17 @@ __global__ __launch_bounds__(kWave) void decode_generic(const DecodeArgs a) {
 
 template <int D, int SG>
 void launch_fast_sg(const DecodeArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
-    if (a.pages.table) hipLaunchKernelGGL((decode_fast<D, SG, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((decode_fast<D, SG, false>), grid, block, 0, stream, a);
+    // The in-kernel split plan (locate_fit) is built for SG <= 2 only: with
+    // more heads per group the matrix-core kernel takes d = 128.
+    if constexpr (SG <= 2) {
+        if (a.fit_items > 0) {
+            if (a.pages.table) hipLaunchKernelGGL((decode_fast<D, SG, true, true>), grid, block, 0, stream, a);
+            else hipLaunchKernelGGL((decode_fast<D, SG, false, true>), grid, block, 0, stream, a);
+            return;
+        }
+    }
+    if (a.pages.table) hipLaunchKernelGGL((decode_fast<D, SG, true, false>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((decode_fast<D, SG, false, false>), grid, block, 0, stream, a);
 }
 
 template <int D>

@@ -29,6 +29,10 @@ CONFIGS = {
     "cfg2": dict(B=16, Hq=32, Hkv=8, d=128, lens=(1024, 8192), dist="normal", append=False),
     "cfg3": dict(B=1, Hq=32, Hkv=8, d=128, lens=(131072, 131072), dist="outlier", append=False),
     "cfg4": dict(B=256, Hq=64, Hkv=8, d=128, lens=(512, 4096), dist="student_t", append=True),
+    # Not a BASELINE.json config: cfg2's ragged lengths with multi-head
+    # attention (every query head its own kv head), the per-lane FMA kernel's
+    # ragged path.
+    "cfg2m": dict(B=16, Hq=32, Hkv=32, d=128, lens=(1024, 8192), dist="normal", append=False),
 }
 
 
