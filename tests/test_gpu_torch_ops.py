@@ -96,13 +96,15 @@ def test_opcheck_decode(o):
                           test_utils=("test_schema", "test_faketensor"))
 
 
-@pytest.mark.parametrize("G", [1, 8])
-def test_decode_graph_capture_replays(o, G):
-    """One decode step (ragged: schedule + decode launches) captured once and
-    replayed three times; q changes eagerly between replays."""
-    rng = np.random.default_rng(6 + G)
-    B, Hkv, cap, d = 4, 2, 1024, 128
-    lengths = np.array([1024, 517, 33, 800], np.int32)
+@pytest.mark.parametrize("G,B", [(1, 4), (8, 4), (8, 80)])
+def test_decode_graph_capture_replays(o, G, B):
+    """One ragged decode step captured once and replayed three times; q
+    changes eagerly between replays.  4 sequences: one launch that plans its
+    splits itself; 80 sequences: the split-schedule launch, then decode."""
+    rng = np.random.default_rng(6 + G + B)
+    Hkv, cap, d = 2, 1024, 128
+    lengths = rng.integers(1, cap + 1, B).astype(np.int32)
+    lengths[:4] = [1024, 517, 33, 800]
     p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, lengths=lengths)
     g = [up(x) for x in (p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths)]
     args = lambda: (g[0], g[1], g[2], g[3], g[4], g[5], cap, 0.0, 0, None, None)
