@@ -37,6 +37,11 @@ constexpr long kMaxCounters = static_cast<long>(kCounterBytes / sizeof(int));
 // its split count rounds down so the grid stays within one round.
 constexpr int kTargetWorkgroupsValu = 256;
 constexpr int kTargetWorkgroupsMfma = 256;
+// Below this many K/V bytes per (sequence, kv head) a chosen split count is 1:
+// a split's merge (record stores, arrival atomic, far reads) costs more than
+// the parallelism saves (B1 H8 d64 L1024: 7.65 us unsplit, 9.8 us in 4
+// splits; from 264 KB per unit the split plans win).
+constexpr long kMinSplitUnitBytes = 192 * 1024;
 // The same for the device split schedule of a ragged batch (work items of
 // equal size, so the target is the number of chunks over the whole batch).
 #ifndef KVQ_SCHED_TARGET_VALU
@@ -150,7 +155,9 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
         // requested may run.
         if (p.fast && splits > 1) chunk = static_cast<int>(round_up(static_cast<size_t>(chunk), gran));
     } else {
-        if (p.kernel == kvq::Kernel::Mfma)
+        if (static_cast<long>(max_len) * (2 * d + 8) < kMinSplitUnitBytes)
+            splits = 1;
+        else if (p.kernel == kvq::Kernel::Mfma)
             splits = std::max<long>(1, kTargetWorkgroupsMfma / units);
         else
             splits = (kTargetWorkgroupsValu + units - 1) / units;
