@@ -1,0 +1,34 @@
+"""bench.py and bench_ops.py command-line contract, checked without a GPU:
+more than one GPU is refused with a message and a non-zero status before any
+device work, and the argument parsers accept every documented option."""
+import os
+import subprocess
+import sys
+
+from _util import REPO
+
+
+def _run(*args):
+    return subprocess.run([sys.executable, *args], cwd=REPO, capture_output=True, text=True, timeout=120)
+
+
+def test_bench_refuses_several_gpus():
+    r = _run("bench.py", "--gpus", "4")
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
+    assert not r.stdout.lstrip().startswith("{")  # no JSON line
+
+
+def test_bench_help_lists_options():
+    r = _run("bench.py", "--help")
+    assert r.returncode == 0
+    for opt in ("--gpus", "--steps", "--warmup", "--settle-ms", "--config", "--splits", "--page-size",
+                "--page-order", "--seed", "--no-cpu", "--cpu-budget"):
+        assert opt in r.stdout, opt
+
+
+def test_bench_ops_help_lists_options():
+    r = _run("bench_ops.py", "--help")
+    assert r.returncode == 0
+    for opt in ("--op", "--M", "--N", "--d", "--B", "--Hkv", "--L", "--dtype", "--steps", "--warmup"):
+        assert opt in r.stdout, opt
