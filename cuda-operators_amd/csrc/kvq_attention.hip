@@ -2,10 +2,10 @@
 // out = softmax(Q K^T / sqrt(d)) V for Q[M,d], K/V[N,d] (one head), the math
 // of the reference's attention_online_launch (attention/softmax_new.cu:87-281).
 //
-// attention_mfma<D> (d in {32, 64, 128}): a workgroup of 8 waves owns 128
-// queries (16 per wave) and one split of the keys, which it streams through
-// LDS in 64-key tiles shared by all its waves (two LDS buffers: one barrier
-// per tile; 135 KB of LDS at d = 128).  Both products run on
+// attention_mfma<D> (d in {32, 64, 128, 256}): a workgroup of 8 waves owns
+// 128 queries (16 per wave) and one split of the keys, which it streams
+// through LDS in 64-key tiles (32 at d = 256) shared by all its waves (two
+// LDS buffers: one barrier per tile; 135 KB of LDS at d = 128).  Both products run on
 // v_mfma_f32_16x16x4_f32 (fp32 in, fp32 accumulate: the same arithmetic as
 // fp32 FMAs, in another order):
 //   * S^T = K Q^T per 16-key block: A = K rows from LDS, B = this wave's q
@@ -40,7 +40,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kAWaves = 8;              // waves per workgroup, 16 queries each
 constexpr int kAQ = 16 * kAWaves;       // queries per workgroup
-constexpr int kAK = 64;                 // keys per LDS tile
+// Keys per LDS tile: 64, or 32 at d = 256 (two double-buffered K/V tiles of
+// 64 x 256 floats would not fit in LDS).
+template <int D>
+constexpr int attention_tile() {
+    return D >= 256 ? 32 : 64;
+}
 constexpr int kAttnMaxSplits = 1024;    // key splits per launch (the merge loops over them)
 
 // Merge of the split records: a group of 2^glog lanes (within one wave) per
@@ -107,9 +112,11 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
     constexpr int NB = D / 16;  // 16-dim output blocks; block c row m = dim NB * m + c
     static_assert(NB % 4 == 0 || NB == 2, "V operand / output vector width");
     constexpr int KS = D + 4;   // LDS row stride in floats (16-byte pad: conflict-free row reads)
-    constexpr int NL = kAK * D / 4 / (kAWaves * kWave);  // float4 per thread per tile per tensor
-    static_assert(NL >= 1, "tile load shape");
-    __shared__ __align__(16) float s_kv[2][2 * kAK * KS];  // two (K tile, V tile) buffers
+    constexpr int AK = attention_tile<D>();  // keys per tile
+    constexpr int KB = AK / 16;              // 16-key blocks per tile
+    constexpr int NL = AK * D / 4 / (kAWaves * kWave);  // float4 per thread per tile per tensor
+    static_assert(NL >= 1 && AK % 16 == 0, "tile load shape");
+    __shared__ __align__(16) float s_kv[2][2 * AK * KS];  // two (K tile, V tile) buffers
     int cur = 0;
 
     const int lane = threadIdx.x & (kWave - 1);
@@ -139,7 +146,7 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
     for (int c = 0; c < NB; c++) o[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
 
-    // Tile loads: float4 f = threadIdx.x + j * 512 of the 64 x D tile.
+    // Tile loads: float4 f = threadIdx.x + j * 512 of the AK x D tile.
     float4 pk[NL], pv[NL];
     auto load_tile = [&](int t0) {
 #pragma unroll
@@ -160,7 +167,7 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
     };
     auto store_tile = [&](int buf) {
         float* const s_k = s_kv[buf];
-        float* const s_v = s_kv[buf] + kAK * KS;
+        float* const s_v = s_kv[buf] + AK * KS;
 #pragma unroll
         for (int j = 0; j < NL; j++) {
             const int f = threadIdx.x + j * kAWaves * kWave;
@@ -176,17 +183,17 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
     if (k0 < k1) {
         load_tile(k0);
         store_tile(0);
-        if (k0 + kAK < k1) load_tile(k0 + kAK);
+        if (k0 + AK < k1) load_tile(k0 + AK);
         __syncthreads();
     }
-    for (int t0 = k0; t0 < k1; t0 += kAK) {
+    for (int t0 = k0; t0 < k1; t0 += AK) {
         const float* const s_k = s_kv[cur];
-        const float* const s_v = s_kv[cur] + kAK * KS;
+        const float* const s_v = s_kv[cur] + AK * KS;
 
-        // S^T for the 4 key blocks: sv[4 kb + i] = score of key t0 + 16 kb + 4 g + i, query r.
-        float sv[16];
+        // S^T for the KB key blocks: sv[4 kb + i] = score of key t0 + 16 kb + 4 g + i, query r.
+        float sv[4 * KB];
 #pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
+        for (int kb = 0; kb < KB; kb++) {
             f32x4 c = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             const float* kr = s_k + (16 * kb + r) * KS + g * DQ;
 #pragma unroll
@@ -205,7 +212,7 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
         }
         float mt = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 16; j++) mt = fmaxf(mt, sv[j]);
+        for (int j = 0; j < 4 * KB; j++) mt = fmaxf(mt, sv[j]);
         mt = fmaxf(mt, __shfl_xor(mt, 16));
         mt = fmaxf(mt, __shfl_xor(mt, 32));
         const float mn = fmaxf(m, mt);
@@ -214,7 +221,7 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
         m = mn;
         l *= alpha;
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
+        for (int j = 0; j < 4 * KB; j++) {
             sv[j] = fast_exp2(sv[j] - ms);
             l += sv[j];
         }
@@ -224,7 +231,7 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
         }
         // O^T += V^T P^T: step (kb, i) contracts keys 16 kb + 4 g + i (k index g).
 #pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
+        for (int kb = 0; kb < KB; kb++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const float* vr = s_v + (16 * kb + 4 * g + i) * KS + NB * r;
@@ -251,9 +258,9 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
         // The next tile (in registers since the previous iteration) goes to the
         // idle buffer, which every wave finished reading before the last
         // barrier; the tile after it starts loading.  One barrier per tile.
-        if (t0 + kAK < k1) {
+        if (t0 + AK < k1) {
             store_tile(cur ^ 1);
-            if (t0 + 2 * kAK < k1) load_tile(t0 + 2 * kAK);
+            if (t0 + 2 * AK < k1) load_tile(t0 + 2 * AK);
         }
         __syncthreads();
         cur ^= 1;
@@ -333,9 +340,9 @@ __global__ __launch_bounds__(kGenWaves* kWave) void attention_generic(const Attn
 
 }  // namespace
 
-int attention_tuned_dim(int d) { return d == 32 || d == 64 || d == 128; }
+int attention_tuned_dim(int d) { return d == 32 || d == 64 || d == 128 || d == 256; }
 int attention_query_block() { return kAQ; }
-int attention_key_tile() { return kAK; }
+int attention_key_tile(int d) { return d >= 256 ? attention_tile<256>() : attention_tile<128>(); }
 int attention_max_splits(int) { return kAttnMaxSplits; }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
@@ -356,9 +363,13 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
                 hipLaunchKernelGGL(attention_mfma<64>, grid, block, 0, stream, a);
                 if (a.splits > 1) hipLaunchKernelGGL(attention_merge<64>, mgrid, mblock, 0, stream, a, glog);
                 break;
-            default:
+            case 128:
                 hipLaunchKernelGGL(attention_mfma<128>, grid, block, 0, stream, a);
                 if (a.splits > 1) hipLaunchKernelGGL(attention_merge<128>, mgrid, mblock, 0, stream, a, glog);
+                break;
+            default:
+                hipLaunchKernelGGL(attention_mfma<256>, grid, block, 0, stream, a);
+                if (a.splits > 1) hipLaunchKernelGGL(attention_merge<256>, mgrid, mblock, 0, stream, a, glog);
                 break;
         }
         return hipGetLastError();

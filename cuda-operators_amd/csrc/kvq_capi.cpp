@@ -374,7 +374,7 @@ AttnPlan attention_plan(int M, int N, int d, bool aligned, int requested) {
     p.tuned = kvq::attention_tuned_dim(d) && aligned;
     p.chunk = N;
     if (!p.tuned) return p;  // the generic kernel runs unsplit
-    const int tile = kvq::attention_key_tile();
+    const int tile = kvq::attention_key_tile(d);
     const long long qblocks = (static_cast<long long>(M) + kvq::attention_query_block() - 1) /
                               kvq::attention_query_block();
     const long long tiles = (static_cast<long long>(N) + tile - 1) / tile;

@@ -154,7 +154,7 @@ struct AttnArgs {
 };
 int attention_tuned_dim(int d);   // the matrix-core kernel handles head dim d
 int attention_query_block();      // queries per matrix-core workgroup
-int attention_key_tile();         // keys per LDS tile
+int attention_key_tile(int d);    // keys per LDS tile of the matrix-core kernel at head dim d
 int attention_max_splits(int d);  // most key splits per matrix-core launch (tuned d)
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 

@@ -4,8 +4,8 @@ attention/softmax_new.cu (kvq_ref_attention_f32, pinned in test_oracle.py).
 
 Tolerance: |gpu - oracle| <= 1e-4 + 1e-3 * |oracle| per element (fp32 with a
 different summation order and exp2 of log2-scaled scores).  Cases: the
-matrix-core head dims (32, 64, 128) with query counts around the 128-query
-block and key counts around the 64-key tile, split and unsplit plans,
+matrix-core head dims (32, 64, 128, 256) with query counts around the
+128-query block and key counts around the 64-key tile (32 at d = 256), split and unsplit plans,
 explicit split requests, untuned head dims and misaligned pointers (generic
 kernel), peaked and flat softmax, workspace reuse across calls, a side
 stream, and at full prefill size a float64 check of sampled rows."""
@@ -39,7 +39,7 @@ def _close(got, ref, what=""):
     np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL, err_msg=what)
 
 
-@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("M,N", [(1, 1), (1, 4099), (7, 64), (128, 65), (129, 300), (200, 1000), (256, 4096),
                                  (1000, 127), (513, 2048)])
 def test_attention_online_tuned(o, d, M, N):
@@ -51,7 +51,7 @@ def test_attention_online_tuned(o, d, M, N):
     _close(down(out), o.attention_f32(q, k, v), f"M={M} N={N} d={d}")
 
 
-@pytest.mark.parametrize("d", [1, 17, 96, 256, 1024])
+@pytest.mark.parametrize("d", [1, 17, 96, 512, 1024])
 def test_attention_online_generic_dims(o, d):
     rng = np.random.default_rng(d)
     M, N = 37, 301
@@ -100,7 +100,7 @@ def test_attention_split_requests(o, splits):
     _close(down(out2), o.attention_f32(q2, k2, v2), f"second call, splits={splits}")
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 128, 256])
 def test_attention_peaked_and_flat(o, d):
     """Large logits (running max changes often, rescales taken) and identical
     keys (uniform weights: the output is the mean of V)."""
