@@ -252,8 +252,10 @@ def main():
         try:
             with open(args.traffic) as f:
                 tr = json.load(f)
-            if tr.get("config") == args.config:
-                traffic = tr.get("hbm_bytes_per_launch")
+            entry = tr.get("configs", {}).get(args.config)
+            # Measured for the contiguous cache with the library's split choice.
+            if entry and args.page_size == 0 and args.splits == 0:
+                traffic = entry.get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
 
