@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--dtype", choices=("f32", "bf16"), default="f32")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=64, help="query rows of the CPU oracle sample")
+    ap.add_argument("--calib", action="store_true",
+                    help="also run one plain 1 GiB copy (torch.mul) to calibrate rocprofv3 byte counters")
     return ap.parse_args()
 
 
@@ -146,6 +148,12 @@ def main():
         sys.exit("bench_ops.py needs a GPU")
     kvq = importlib.import_module("cuda-operators_amd").kvq
     line = bench_attention(torch, kvq, a) if a.op == "attention" else bench_prefill(torch, kvq, a)
+    if a.calib:
+        x = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+        y = torch.empty_like(x)
+        torch.mul(x, 1.0, out=y)
+        torch.cuda.synchronize()
+        del x, y
     print(json.dumps(line), flush=True)
 
 
