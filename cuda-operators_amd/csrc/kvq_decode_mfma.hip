@@ -53,7 +53,6 @@ typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
 constexpr int kMWaves = 4;        // waves per workgroup
 constexpr int kMTile = 32;        // tokens per wave tile
-constexpr int kMD = 128;          // head dim
 constexpr float kPScale = 32768.0f;  // PV weights are formed in [-2^15, 2^15] before the f16 split
 constexpr int kMBStep = kMTile * kMWaves;
 
@@ -79,21 +78,35 @@ __device__ __forceinline__ int pack_bytes(const int* b) {
            static_cast<int>(static_cast<unsigned>(b[3] & 0xff) << 24);
 }
 
-template <int G, bool PAGED, bool FIT>
+// Piece slot of 16-byte piece p of V row rw in an LDS tile (rows of D / 16
+// pieces): the 8 rows one transposed read takes (4g .. 4g+3 and
+// 16+4g .. 16+4g+3) land in 8 different 16-byte bank groups.
+template <int D>
+__device__ __forceinline__ int v_slot(int p, int rw) {
+    if constexpr (D == 128) return p ^ (rw & 7);
+    else return p ^ (((rw >> 1) & 1) | ((rw >> 3) & 2));
+}
+
+template <int D, int G, bool PAGED, bool FIT>
 __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma(
     const DecodeArgs a) {
     static_assert(G == 4 || G == 8, "heads per workgroup");
-    static_assert(2 * kMD == 4 * kWave, "the fused append gives 4 K/V elements to each lane of a wave");
+    static_assert(D == 64 || D == 128, "head dims of the matrix-core decode kernel");
+    constexpr int NJ = D / 64;            // 64-dim blocks of a K row (QK k-steps, q limb blocks)
+    constexpr int NB = D / 16;            // 16-byte pieces of a row (PV blocks)
+    constexpr int RPLV = kWave / NB;      // V rows one tile load instruction covers
+    constexpr int NV = kMTile / RPLV;     // V load instructions per tile
+    constexpr int NE = 2 * D / kWave;     // appended K+V elements per lane of the owning wave
     // V tile buffers during the tile loop; the waves' results afterwards.
     union TileOrResult {
-        int8_t v[kMWaves][2][kMTile * kMD];
-        float acc[kMWaves][16][kMD];
+        int8_t v[kMWaves][2][kMTile * D];
+        float acc[kMWaves][16][D];
     };
     __shared__ __align__(16) TileOrResult s_u;
     auto& s_v = s_u.v;
     auto& s_acc = s_u.acc;
     __shared__ float s_ml[kMWaves][G][2];
-    __shared__ __align__(16) int8_t s_newq[2][kMD];
+    __shared__ __align__(16) int8_t s_newq[2][D];
     __shared__ int s_last;
 
     const int lane = threadIdx.x & (kWave - 1);
@@ -119,7 +132,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     const int nsplit = w.nsplit;
 
     if (len == 0) {
-        for (int i = threadIdx.x; i < G * kMD; i += blockDim.x) a.out[bhq0 * kMD + i] = 0.0f;
+        for (int i = threadIdx.x; i < G * D; i += blockDim.x) a.out[bhq0 * D + i] = 0.0f;
         return;
     }
 
@@ -131,22 +144,22 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
 
     // Fused append: the wave whose tiles include token len-1 (wave w's tiles
     // start at t0 + 32 w + 128 i) quantises the new token on its own; its fp32
-    // row is fetched first (element lane + 64 j: j < 2 of K, j >= 2 of V).
+    // row is fetched first (element lane + 64 j: j < NJ of K, j >= NJ of V).
     const bool own_new = app && ((tnew - t0) / kMTile) % kMWaves == wave;
-    float xnew[4];
+    float xnew[NE];
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-        xnew[j] = own_new ? (j < 2 ? a.k_new : a.v_new)[static_cast<size_t>(bh) * kMD + ((lane + kWave * j) & (kMD - 1))]
+    for (int j = 0; j < NE; j++)
+        xnew[j] = own_new ? (j < NJ ? a.k_new : a.v_new)[static_cast<size_t>(bh) * D + ((lane + kWave * j) & (D - 1))]
                           : 0.0f;
 
     // q of head (r % G) as int8 limbs in the QK B operand layout:
     // qb[j][limb] holds dims 64j + 16g + [0,16).
     const int hrow = r % G;
-    float qv[32];
+    float qv[16 * NJ];
     {
-        const float* qp = a.q + (bhq0 + hrow) * kMD + 16 * g;
+        const float* qp = a.q + (bhq0 + hrow) * D + 16 * g;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < NJ; j++) {
 #pragma unroll
             for (int i4 = 0; i4 < 4; i4++) {
                 const float4 x = *reinterpret_cast<const float4*>(qp + 64 * j + 4 * i4);
@@ -160,12 +173,12 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // The limbs are formed after the first tile's loads are issued (their
     // latency overlaps this work); qs turns an integer dot into a score in
     // log2 units (after x k_scale).
-    i32x4 qb[2][3];
+    i32x4 qb[NJ][3];
     float qs = 0.0f;
     auto prepare_q = [&]() {
         float qmax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 32; i++) qmax = fmaxf(qmax, fabsf(qv[i]));
+        for (int i = 0; i < 16 * NJ; i++) qmax = fmaxf(qmax, fabsf(qv[i]));
         qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
         qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
         int qexp = 0;
@@ -173,7 +186,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         const int E = qmax > 0.0f ? min(max(22 - qexp, -100), 126) : 0;
         qs = ldexpf(1.0f, -E) * a.scale_log2;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < NJ; j++) {
             int limb[3][16];
 #pragma unroll
             for (int i = 0; i < 16; i++) {
@@ -198,9 +211,9 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // [-1, 1].  acc[c] holds O^T[16c + 4g + i][row r] in units of
     // vref / kPScale.
     float m = -INFINITY, lsum = 0.0f, vref = 0.0f;
-    f32x4 acc[8];
+    f32x4 acc[NB];
 #pragma unroll
-    for (int c = 0; c < 8; c++) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < NB; c++) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const bool lo_row = ((r / G) & 1) != 0;
 
     // This (batch, kv head)'s cache rows as buffer resources: tile loads add a
@@ -208,8 +221,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // reads past the capacity return 0.  A paged cache gets resources per
     // tile instead (below).
     const unsigned cap = static_cast<unsigned>(a.cap);
-    const buf_rsrc kres = make_rsrc(a.k + row0 * kMD, cap * kMD);
-    const buf_rsrc vres = make_rsrc(a.v + row0 * kMD, cap * kMD);
+    const buf_rsrc kres = make_rsrc(a.k + row0 * D, cap * D);
+    const buf_rsrc vres = make_rsrc(a.v + row0 * D, cap * D);
     const buf_rsrc ksres = make_rsrc(a.ks + row0, cap * 4u);
     const buf_rsrc vsres = make_rsrc(a.vs + row0, cap * 4u);
 
@@ -226,15 +239,21 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     float newks = 0.0f, newvs = 0.0f;
     auto append_new = [&]() {
         const size_t rnew = PAGED ? cache_row(a.pages, a.Hkv, a.cap, b, kvh, tnew) : row0 + tnew;
-        newks = quant_scale(wave_max(fmaxf(fabsf(xnew[0]), fabsf(xnew[1]))));
-        newvs = quant_scale(wave_max(fmaxf(fabsf(xnew[2]), fabsf(xnew[3]))));
+        float amk = fabsf(xnew[0]), amv = fabsf(xnew[NJ]);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            s_newq[j >> 1][lane + kWave * (j & 1)] = static_cast<int8_t>(quant_one(xnew[j], j < 2 ? newks : newvs));
+        for (int j = 1; j < NJ; j++) {
+            amk = fmaxf(amk, fabsf(xnew[j]));
+            amv = fmaxf(amv, fabsf(xnew[NJ + j]));
+        }
+        newks = quant_scale(wave_max(amk));
+        newvs = quant_scale(wave_max(amv));
+#pragma unroll
+        for (int j = 0; j < NE; j++)
+            s_newq[j / NJ][lane + kWave * (j % NJ)] = static_cast<int8_t>(quant_one(xnew[j], j < NJ ? newks : newvs));
         if (sgi == 0) {
-            if (lane < 16) {
-                const int row = lane >> 3, piece = lane & 7;
-                *reinterpret_cast<int4*>((row ? a.v : a.k) + rnew * kMD + 16 * piece) =
+            if (lane < 2 * NB) {
+                const int row = lane / NB, piece = lane % NB;
+                *reinterpret_cast<int4*>((row ? a.v : a.k) + rnew * D + 16 * piece) =
                     *reinterpret_cast<const int4*>(&s_newq[row][16 * piece]);
             }
             if (lane == 0) {
@@ -247,8 +266,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // One tile's global data in registers: K sub-tiles (A operand of QK), the
     // 32 V rows (16 bytes per lane) and the scales of tokens base+16s+4g+i.
     struct Tile {
-        i32x4 ka[2][2];
-        int4 v[4];
+        i32x4 ka[2][NJ];
+        int4 v[NV];
         float ks[2][4], vs[2][4];
     };
     const int wbase = t0 + __builtin_amdgcn_readfirstlane(wave) * kMTile;  // wave-uniform
@@ -256,12 +275,12 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // Lane byte offsets within a tile: K row r, dims 16g.. (+64 for the second
     // 64-dim block, +16 rows for sub-tile 1); V row lane/8, 16-byte piece
     // lane%8 (+8 rows per c); scales of tokens 4g..4g+3 (+16 tokens for s = 1).
-    const int kvo = r * kMD + 16 * g;
-    const int vvo = (lane >> 3) * kMD + 16 * (lane & 7);
+    const int kvo = r * D + 16 * g;
+    const int vvo = (lane / NB) * D + 16 * (lane % NB);
     const int svo = 16 * g;
     auto load_tile = [&](Tile& T, int it) {
         const int base = wbase + it * kMBStep;
-        int ko = base * kMD;
+        int ko = base * D;
         int so = base * 4;
         buf_rsrc kr = kres, vr = vres, ksr = ksres, vsr = vsres;
         if constexpr (PAGED) {
@@ -269,20 +288,20 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             // from its first token to the end of that page.
             const size_t rp = cache_row(a.pages, a.Hkv, a.cap, b, kvh, base);
             const unsigned rem = static_cast<unsigned>(a.pages.size - (base & (a.pages.size - 1)));
-            kr = make_rsrc(a.k + rp * kMD, rem * kMD);
-            vr = make_rsrc(a.v + rp * kMD, rem * kMD);
+            kr = make_rsrc(a.k + rp * D, rem * D);
+            vr = make_rsrc(a.v + rp * D, rem * D);
             ksr = make_rsrc(a.ks + rp, rem * 4u);
             vsr = make_rsrc(a.vs + rp, rem * 4u);
             ko = so = 0;
         }
 #pragma unroll
         for (int s = 0; s < 2; s++) {
-            T.ka[s][0] = buffer_load16_stream(kr, kvo + s * 16 * kMD, ko);
-            T.ka[s][1] = buffer_load16_stream(kr, kvo + s * 16 * kMD + 64, ko);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) T.ka[s][j] = buffer_load16_stream(kr, kvo + s * 16 * D + 64 * j, ko);
         }
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const v4i_t x = buffer_load16_stream(vr, vvo + c * 8 * kMD, ko);
+        for (int c = 0; c < NV; c++) {
+            const v4i_t x = buffer_load16_stream(vr, vvo + c * RPLV * D, ko);
             T.v[c] = make_int4(x.x, x.y, x.z, x.w);
         }
 #pragma unroll
@@ -301,10 +320,10 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // bank groups.
     auto stage_v = [&](const Tile& T, int8_t* vt) {
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int rw = 8 * c + (lane >> 3);
-            const int p = lane & 7;
-            *reinterpret_cast<int4*>(vt + rw * kMD + ((p ^ (rw & 7)) << 4)) = T.v[c];
+        for (int c = 0; c < NV; c++) {
+            const int rw = RPLV * c + lane / NB;
+            const int p = lane % NB;
+            *reinterpret_cast<int4*>(vt + rw * D + (v_slot<D>(p, rw) << 4)) = T.v[c];
         }
     };
     // The appended token replaces what the cache held at position len-1 (only
@@ -314,8 +333,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             if (base + 16 * s + r == tnew) {
-                T.ka[s][0] = *reinterpret_cast<const i32x4*>(&s_newq[0][16 * g]);
-                T.ka[s][1] = *reinterpret_cast<const i32x4*>(&s_newq[0][64 + 16 * g]);
+#pragma unroll
+                for (int j = 0; j < NJ; j++) T.ka[s][j] = *reinterpret_cast<const i32x4*>(&s_newq[0][64 * j + 16 * g]);
             }
 #pragma unroll
             for (int i = 0; i < 4; i++)
@@ -325,8 +344,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
                 }
         }
         const int rw = tnew - base;
-        if (rw >= 0 && rw < kMTile && lane < 8)
-            *reinterpret_cast<int4*>(vt + rw * kMD + ((lane ^ (rw & 7)) << 4)) =
+        if (rw >= 0 && rw < kMTile && lane < NB)
+            *reinterpret_cast<int4*>(vt + rw * D + (v_slot<D>(lane, rw) << 4)) =
                 *reinterpret_cast<const int4*>(&s_newq[1][16 * lane]);
     };
     // check_tail: the tile may reach past tend (only a wave's last tile can).
@@ -338,8 +357,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
             for (int lb = 0; lb < 3; lb++) {
                 i32x4 c = i32x4{0, 0, 0, 0};
-                c = __builtin_amdgcn_mfma_i32_16x16x64_i8(T.ka[s][0], qb[0][lb], c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_i32_16x16x64_i8(T.ka[s][1], qb[1][lb], c, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < NJ; j++) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(T.ka[s][j], qb[j][lb], c, 0, 0, 0);
                 cq[s][lb] = c;
             }
         }
@@ -391,7 +410,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         vref = vn;
         if (__builtin_amdgcn_ballot_w64(f != 1.0f) != 0) {  // a row's max or vref moved
 #pragma unroll
-            for (int c = 0; c < 8; c++) acc[c] *= f;
+            for (int c = 0; c < NB; c++) acc[c] *= f;
         }
         // P^T as the PV B operand: row r takes the hi or lo f16 part of
         // w = p * v_scale * kPScale / vref.
@@ -407,10 +426,10 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             pb[k] = lo_row ? lo : hi;
         }
         lsum = lsum * alpha + ps;
-        // PV: 8 blocks of 16 dims.
+        // PV: D / 16 blocks of 16 dims.
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const int8_t* src = vt + vrow * kMD + ((c ^ (vrow & 7)) << 4) + 8 * h2;
+        for (int c = 0; c < NB; c++) {
+            const int8_t* src = vt + vrow * D + (v_slot<D>(c, vrow) << 4) + 8 * h2;
             const i32x2 vb = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(const_cast<int8_t*>(src)));
             acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_f16(vb), pb, acc[c], 0, 0, 0);
         }
@@ -456,7 +475,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     __syncthreads();  // every wave is done with its V tiles (s_acc reuses them)
     const float fct = vref * (1.0f / kPScale);
 #pragma unroll
-    for (int c = 0; c < 8; c++) {
+    for (int c = 0; c < NB; c++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) s_acc[wave][r][16 * c + 4 * g + i] = acc[c][i] * fct;
     }
@@ -472,9 +491,9 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         if constexpr (FIT) map = rec_map_fit(a, w, bhq0);
         else map = rec_map(a, b, bhq0);
     }
-    for (int i = threadIdx.x; i < G * kMD; i += blockDim.x) {
-        const int h = i / kMD;
-        const int dim = i - h * kMD;
+    for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
+        const int h = i / D;
+        const int dim = i - h * D;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < kMWaves; w++) M = fmaxf(M, s_ml[w][h][0]);
@@ -496,38 +515,34 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
 int mfma_tile_tokens() { return kMBStep; }
 
 int mfma_heads_per_group(int G, int d) {
-    if (d != kMD) return 0;
+    if (d != 64 && d != 128) return 0;
     if (G % 8 == 0) return 8;
     if (G % 4 == 0) return 4;
     return 0;
 }
 
+namespace {
+template <int D, int G>
+void launch_mfma_dg(const DecodeArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+    const bool paged = a.pages.table != nullptr;
+    if (a.fit_items > 0) {
+        if (paged) hipLaunchKernelGGL((decode_mfma<D, G, true, true>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((decode_mfma<D, G, false, true>), grid, block, 0, stream, a);
+    } else {
+        if (paged) hipLaunchKernelGGL((decode_mfma<D, G, true, false>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((decode_mfma<D, G, false, false>), grid, block, 0, stream, a);
+    }
+}
+}  // namespace
+
 hipError_t launch_decode_mfma(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(decode_grid(a, p)));
     const dim3 block(kMWaves * kWave);
-    const bool paged = a.pages.table != nullptr;
-    const bool fit = a.fit_items > 0;
-    switch (p.sg) {
-        case 4:
-            if (fit) {
-                if (paged) hipLaunchKernelGGL((decode_mfma<4, true, true>), grid, block, 0, stream, a);
-                else hipLaunchKernelGGL((decode_mfma<4, false, true>), grid, block, 0, stream, a);
-            } else {
-                if (paged) hipLaunchKernelGGL((decode_mfma<4, true, false>), grid, block, 0, stream, a);
-                else hipLaunchKernelGGL((decode_mfma<4, false, false>), grid, block, 0, stream, a);
-            }
-            break;
-        case 8:
-            if (fit) {
-                if (paged) hipLaunchKernelGGL((decode_mfma<8, true, true>), grid, block, 0, stream, a);
-                else hipLaunchKernelGGL((decode_mfma<8, false, true>), grid, block, 0, stream, a);
-            } else {
-                if (paged) hipLaunchKernelGGL((decode_mfma<8, true, false>), grid, block, 0, stream, a);
-                else hipLaunchKernelGGL((decode_mfma<8, false, false>), grid, block, 0, stream, a);
-            }
-            break;
-        default: return hipErrorInvalidValue;
-    }
+    if (a.d == 128 && p.sg == 4) launch_mfma_dg<128, 4>(a, grid, block, stream);
+    else if (a.d == 128 && p.sg == 8) launch_mfma_dg<128, 8>(a, grid, block, stream);
+    else if (a.d == 64 && p.sg == 4) launch_mfma_dg<64, 4>(a, grid, block, stream);
+    else if (a.d == 64 && p.sg == 8) launch_mfma_dg<64, 8>(a, grid, block, stream);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

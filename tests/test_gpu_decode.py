@@ -125,7 +125,8 @@ def test_softmax_scale_override(o):
     assert_close(got, want, what="softmax_scale")
 
 
-@pytest.mark.parametrize("d,G", [(64, 2), (128, 2), (256, 2), (96, 2), (128, 4), (128, 8), (128, 16)])
+@pytest.mark.parametrize("d,G", [(64, 2), (128, 2), (256, 2), (96, 2), (128, 4), (128, 8), (128, 16), (64, 4),
+                                 (64, 8)])
 def test_fused_append_matches_separate_append(o, d, G):
     """Fused append inside the decode kernel == kvq_append_launch followed by decode:
     bit-for-bit in the cache; the outputs agree to fp32 rounding (the new token
@@ -203,10 +204,11 @@ def test_side_stream(o):
 
 @pytest.mark.parametrize("splits", [1, 3, 8])
 @pytest.mark.parametrize("G", [4, 8])
-def test_mfma_splits_with_fused_append(o, G, splits):
+@pytest.mark.parametrize("d", [64, 128])
+def test_mfma_splits_with_fused_append(o, d, G, splits):
     """Grouped-query (matrix-core) path: fused append in the last split, split merge."""
-    rng = np.random.default_rng(100 * G + splits)
-    B, Hkv, cap, d = 3, 2, 1500, 128
+    rng = np.random.default_rng(100 * G + splits + d)
+    B, Hkv, cap = 3, 2, 1500
     lengths = np.array([1500, 33, 1025], np.int32)
     p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, dist="student_t", lengths=lengths)
     kn = rng.standard_t(4, (B, Hkv, d)).astype(np.float32)
@@ -217,13 +219,14 @@ def test_mfma_splits_with_fused_append(o, G, splits):
     assert np.array_equal(gk, p["k"]) and np.array_equal(gv, p["v"])
     assert np.array_equal(_bits(gks), _bits(p["ks"])) and np.array_equal(_bits(gvs), _bits(p["vs"]))
     want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
-    assert_close(got, want, what=f"mfma G={G} splits={splits}")
+    assert_close(got, want, what=f"mfma d={d} G={G} splits={splits}")
 
 
-def test_mfma_extreme_scales(o):
+@pytest.mark.parametrize("d", [64, 128])
+def test_mfma_extreme_scales(o, d):
     """Tiny, huge and zero per-token scales and a large |q| on the matrix-core path."""
-    rng = np.random.default_rng(77)
-    B, Hkv, G, cap, d = 1, 2, 8, 300, 128
+    rng = np.random.default_rng(77 + d)
+    B, Hkv, G, cap = 1, 2, 8, 300
     p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows)
     p["vs"][0, 0, :50] = np.float32(1e-30)
     p["vs"][0, 0, 50:60] = np.float32(0.0)
@@ -236,13 +239,14 @@ def test_mfma_extreme_scales(o):
 
 
 @pytest.mark.parametrize("splits", [1, 5])
-def test_mfma_ignores_slots_past_length(o, splits):
+@pytest.mark.parametrize("d", [64, 128])
+def test_mfma_ignores_slots_past_length(o, d, splits):
     """Cache slots past each sequence's length hold NaN/Inf scales and the last
     tile of a wave reaches into them (and past the capacity): they must get no
     weight.  Also negative v scales, which the weight normalisation takes by
     magnitude."""
-    rng = np.random.default_rng(31 + splits)
-    B, Hkv, G, cap, d = 4, 2, 4, 1028, 128
+    rng = np.random.default_rng(31 + splits + d)
+    B, Hkv, G, cap = 4, 2, 4, 1028
     lengths = np.array([1028, 1, 161, 700], np.int32)
     p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, lengths=lengths)
     for b, n in enumerate(lengths):

@@ -96,6 +96,7 @@ CASES = [  # (G, d, page): MFMA needs d = 128, G % 4 == 0 and a power-of-two pag
     (2, 64, 32), (1, 256, 16), (1, 32, 64),     # multiple of its wave tile; anything else runs
     (4, 128, 32), (8, 128, 128), (4, 128, 64),  # the generic kernel.
     (1, 128, 24), (4, 128, 48), (8, 128, 16), (1, 32, 16), (3, 96, 32),
+    (4, 64, 32), (8, 64, 128),
 ]
 
 
@@ -112,7 +113,7 @@ def test_paged_matches_oracle(o, G, d, page):
 
 
 @pytest.mark.parametrize("G,d,page,splits", [(1, 128, 32, 0), (1, 128, 64, 3), (8, 128, 32, 0),
-                                             (4, 128, 128, 5), (2, 64, 64, 0), (1, 256, 16, 2)])
+                                             (4, 128, 128, 5), (2, 64, 64, 0), (1, 256, 16, 2), (8, 64, 64, 3)])
 def test_paged_bitwise_equals_contiguous(o, G, d, page, splits):
     """Same tuned kernel, same splits: identical bits to the contiguous layout."""
     rng = np.random.default_rng(100 + G + d + page + splits)
@@ -125,7 +126,8 @@ def test_paged_bitwise_equals_contiguous(o, G, d, page, splits):
     assert np.array_equal(_bits(got), _bits(ref))
 
 
-@pytest.mark.parametrize("G,d,page", [(1, 128, 32), (8, 128, 32), (4, 128, 128), (2, 64, 16), (3, 96, 32)])
+@pytest.mark.parametrize("G,d,page", [(1, 128, 32), (8, 128, 32), (4, 128, 128), (2, 64, 16), (3, 96, 32),
+                                      (4, 64, 32)])
 def test_paged_fused_append(o, G, d, page):
     """The new token lands in its page slot with the oracle's bits; the output
     attends over it."""

@@ -37,7 +37,7 @@ def _ragged_lengths(rng, B, cap):
 
 
 @pytest.mark.parametrize("append", [False, True])
-@pytest.mark.parametrize("G,d", [(1, 128), (2, 64), (4, 128), (8, 128), (1, 256), (4, 32)])
+@pytest.mark.parametrize("G,d", [(1, 128), (2, 64), (4, 128), (8, 128), (1, 256), (4, 32), (4, 64), (8, 64)])
 def test_schedule_ragged(o, G, d, append):
     """VALU (G = 1, 2; d 32..256) and matrix-core (G = 4, 8 at d = 128) kernels."""
     rng = np.random.default_rng(1000 * G + d + append)
