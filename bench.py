@@ -135,7 +135,7 @@ def paged_decoder(kvq, p, out, page, splits, seed, order="shuffled"):
 def kernel_name(base, page):
     """The tuned kernel the library's planner picks for this problem."""
     G = base.Hq // base.Hkv
-    mfma = base.d == 128 and G % 4 == 0 and (page == 0 or (page & (page - 1) == 0 and page % 32 == 0))
+    mfma = base.d in (64, 128) and G % 4 == 0 and (page == 0 or (page & (page - 1) == 0 and page % 32 == 0))
     name = "decode_mfma" if mfma else "decode_fast"
     if base.uniform:
         return name
