@@ -141,6 +141,31 @@ def test_workspace_sizes(L):
     assert L.kvq_decode_workspace_size(ctypes.byref(p)) > 0
 
 
+def _ru(x, a=256):
+    return (x + a - 1) // a * a
+
+
+@pytest.mark.parametrize("B", [24, 64, 65, 1025])
+def test_matrix_core_plan_by_workspace(L, B):
+    """Grouped-query heads at d = 128 (matrix-core kernel, 4 heads per
+    workgroup, U = Hkv work units per sequence), ragged lengths: up to 64
+    sequences the kernel plans the batch itself, with 256 / U items of
+    records; beyond that the device split schedule's words come on top of
+    its own B + 512 / U + 1 items of records.  Records hold (d + 2) floats
+    per query head after the counter block."""
+    Hq, Hkv, d = 8, 2, 128
+    p = _params(batch=B, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=d, lengths=FAKE, capacity=512,
+                max_seq_len=512)
+    n = L.kvq_decode_workspace_size(ctypes.byref(p))
+    if B <= 64:
+        items = 256 // Hkv
+        assert n == 256 * 1024 + _ru(items * Hq * 2 * 4) + _ru(items * Hq * d * 4)
+    else:
+        items = B + (512 + Hkv - 1) // Hkv + 1
+        sched = _ru((4 + 2 * items + 2 * B) * 4)
+        assert n == 256 * 1024 + sched + _ru(items * Hq * 2 * 4) + _ru(items * Hq * d * 4)
+
+
 def test_append_and_quantize_reject_before_hip(L):
     bad = kvq.AppendParams(2, 2, 128, 16, None, 0, None, FAKE, FAKE, FAKE, FAKE, FAKE)
     assert L.kvq_append_launch(ctypes.byref(bad), None) == INVALID

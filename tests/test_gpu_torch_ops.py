@@ -96,11 +96,12 @@ def test_opcheck_decode(o):
                           test_utils=("test_schema", "test_faketensor"))
 
 
-@pytest.mark.parametrize("G,B", [(1, 4), (8, 4), (8, 80)])
+@pytest.mark.parametrize("G,B", [(1, 4), (1, 80), (8, 4), (8, 80)])
 def test_decode_graph_capture_replays(o, G, B):
     """One ragged decode step captured once and replayed three times; q
     changes eagerly between replays.  4 sequences: one launch that plans its
-    splits itself; 80 sequences: the split-schedule launch, then decode."""
+    splits itself; 80 sequences: the split-schedule launch, then decode (FMA
+    kernel for G = 1, matrix-core kernel for G = 8)."""
     rng = np.random.default_rng(6 + G + B)
     Hkv, cap, d = 2, 1024, 128
     lengths = rng.integers(1, cap + 1, B).astype(np.int32)
