@@ -36,7 +36,10 @@ constexpr long kMaxCounters = static_cast<long>(kCounterBytes / sizeof(int));
 // one (cfg3: 48.0 us at 256 workgroups, 52.0 us at 512, 62.3 us at 384), and
 // its split count rounds down so the grid stays within one round.
 constexpr int kTargetWorkgroupsValu = 256;
-constexpr int kTargetWorkgroupsMfma = 256;
+#ifndef KVQ_TARGET_WG_MFMA
+#define KVQ_TARGET_WG_MFMA 256
+#endif
+constexpr int kTargetWorkgroupsMfma = KVQ_TARGET_WG_MFMA;
 // Below this many K/V bytes per (sequence, kv head) a chosen split count is 1:
 // a split's merge (record stores, arrival atomic, far reads) costs more than
 // the parallelism saves (B1 H8 d64 L1024: 7.65 us unsplit, 9.8 us in 4

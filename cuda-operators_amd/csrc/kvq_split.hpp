@@ -229,6 +229,7 @@ __device__ __forceinline__ void store_result(const DecodeArgs& a, const RecMap& 
 constexpr int kMergeHeads = 8;
 constexpr int kMergeSplits = 256;
 constexpr int kMergeMaxThreads = 512;
+constexpr int kMergePairsPerThread = 8;  // (m, l) loads per thread in phase 1
 constexpr int kCoherent = 16;  // buffer-load cache policy: sc1, device-coherent (as get_coherent)
 
 // Records spanned by the group's merge (relative to map.r0).
@@ -238,7 +239,8 @@ __device__ __forceinline__ long merge_span(const RecMap& map, int nheads, int ns
 
 __device__ inline bool merge_group_fits(const DecodeArgs& a, const RecMap& map, int nheads, int nsplit) {
     return nheads <= kMergeHeads && nsplit <= kMergeSplits && (a.d & 3) == 0 &&
-           merge_span(map, nheads, nsplit) * a.d < (1L << 29) && blockDim.x <= kMergeMaxThreads;
+           merge_span(map, nheads, nsplit) * a.d < (1L << 29) && blockDim.x <= kMergeMaxThreads &&
+           nheads * nsplit <= kMergePairsPerThread * static_cast<int>(blockDim.x);
 }
 
 __device__ inline void merge_group(const DecodeArgs& a, const RecMap& map, size_t bhq0, int nheads, int nsplit) {
@@ -260,9 +262,9 @@ __device__ inline void merge_group(const DecodeArgs& a, const RecMap& map, size_
     const buf_rsrc mlr = make_rsrc(a.part_ml + map.r0 * 2, span * 8u);
     const buf_rsrc accr = make_rsrc(a.part_acc + map.r0 * d, span * static_cast<unsigned>(d) * 4u);
 
-    const int npairs = nheads * nsplit;  // <= 2048, so at most 8 per thread
+    const int npairs = nheads * nsplit;  // <= kMergePairsPerThread * T (merge_group_fits)
 #pragma unroll
-    for (int k = 0; k < kMergeHeads * kMergeSplits / 256; k++) {
+    for (int k = 0; k < kMergePairsPerThread; k++) {
         const int i = t + k * T;
         if (i < npairs) {
             const int h = i / nsplit;
