@@ -156,7 +156,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              f"(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              f"(sharding across GPUs is designed, not built)", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -1,10 +1,10 @@
 // kvq_decode_mfma.hip -- grouped-query decode attention on gfx950 matrix cores.
 //
 // For G query heads sharing a kv head the per-token work is a small dense
-// contraction (QK: [G x 128] x [128 x T], PV: [G x T] x [T x 128]), so with
-// G = 4 or 8 it runs on MFMA instead of per-lane FMAs.  Same math and result
+// contraction (QK: [G x D] x [D x T], PV: [G x T] x [T x D]), so with G = 4
+// or 8 it runs on MFMA instead of per-lane FMAs.  Same math and result
 // contract as decode_fast (the reference's cpu_reference per query head,
-// kv_cache/KV_int8_split_optimized.cu:385-437); head_dim 128.
+// kv_cache/KV_int8_split_optimized.cu:385-437); head dim D = 64 or 128.
 //
 // One workgroup (4 waves) per (sequence split, batch, kv head, group of G
 // query heads); each wave walks 32-token tiles with its own online-softmax
