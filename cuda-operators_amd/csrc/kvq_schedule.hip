@@ -75,11 +75,14 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
     __shared__ int s_tmp[kSchedWaves];
     __shared__ long long s_sum[kSchedWaves];
     __shared__ int s_class[kSizeClasses];
-    __shared__ int s_len[kSchedThreads];
+    __shared__ int s_len[kSchedThreads];  // the first kSchedThreads clamped lengths
     __shared__ int s_best;
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
     const int wave = t / kWave;
+    // Length of sequence b: from LDS after the first pass (one read of the
+    // lengths for batches up to kSchedThreads), from memory beyond that.
+    auto len_of = [&](int b) { return b < kSchedThreads ? s_len[b] : clamped_len(lengths, b, max_len); };
 
     long long sum = 0;
     for (int b = t; b < B; b += kSchedThreads) {
@@ -146,7 +149,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
         const int b = b0 + t;
         int len = 0, n = 0;
         if (b < B) {
-            len = clamped_len(lengths, b, max_len);
+            len = len_of(b);
             n = len == 0 ? 1 : (len + chunk - 1) / chunk;
         }
         const int full = n > 0 ? n - 1 : 0;
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
     }
     __syncthreads();
     for (int b = t; b < B; b += kSchedThreads) {
-        const int len = clamped_len(lengths, b, max_len);
+        const int len = len_of(b);
         const int n = len == 0 ? 1 : (len + chunk - 1) / chunk;
         const int last = len - (n - 1) * chunk;
         const int cls = static_cast<int>(static_cast<long long>(chunk - last) * kSizeClasses / (chunk + 1));
