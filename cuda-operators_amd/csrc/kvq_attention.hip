@@ -38,8 +38,8 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kAWaves = 8;              // waves per workgroup, 16 queries each
-constexpr int kAQ = 16 * kAWaves;       // queries per workgroup
+// Waves per workgroup (16 queries each): kAttnBlockWide / 16, or
+// kAttnBlockNarrow / 16 when the wide blocks cannot fill the GPU.
 // Keys per LDS tile: 64, or 32 at d = 256 (two double-buffered K/V tiles of
 // 64 x 256 floats would not fit in LDS).
 template <int D>
@@ -106,15 +106,15 @@ __global__ __launch_bounds__(kMergeThreads) void attention_merge(const AttnArgs 
     }
 }
 
-template <int D>
-__global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs a) {
+template <int D, int W>
+__global__ __launch_bounds__(W* kWave) void attention_mfma(const AttnArgs a) {
     constexpr int DQ = D / 4;   // contraction dims per lane group in QK
     constexpr int NB = D / 16;  // 16-dim output blocks; block c row m = dim NB * m + c
     static_assert(NB % 4 == 0 || NB == 2, "V operand / output vector width");
     constexpr int KS = D + 4;   // LDS row stride in floats (16-byte pad: conflict-free row reads)
     constexpr int AK = attention_tile<D>();  // keys per tile
     constexpr int KB = AK / 16;              // 16-key blocks per tile
-    constexpr int NL = AK * D / 4 / (kAWaves * kWave);  // float4 per thread per tile per tensor
+    constexpr int NL = AK * D / 4 / (W * kWave);  // float4 per thread per tile per tensor
     static_assert(NL >= 1 && AK % 16 == 0, "tile load shape");
     __shared__ __align__(16) float s_kv[2][2 * AK * KS];  // two (K tile, V tile) buffers
     int cur = 0;
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
     const int r = lane & 15;
     const int g = lane >> 4;
     const int split = blockIdx.y;
-    const int q0 = blockIdx.x * kAQ + wave * 16;
+    const int q0 = blockIdx.x * (16 * W) + wave * 16;
     const int k0 = split * a.chunk;
     const int k1 = min(a.N, k0 + a.chunk);
 
@@ -146,12 +146,12 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
     for (int c = 0; c < NB; c++) o[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
 
-    // Tile loads: float4 f = threadIdx.x + j * 512 of the AK x D tile.
+    // Tile loads: float4 f = threadIdx.x + j * (64 W) of the AK x D tile.
     float4 pk[NL], pv[NL];
     auto load_tile = [&](int t0) {
 #pragma unroll
         for (int j = 0; j < NL; j++) {
-            const int f = threadIdx.x + j * kAWaves * kWave;
+            const int f = threadIdx.x + j * W * kWave;
             const int row = f / (D / 4);
             const int c4 = f - row * (D / 4);
             const int key = t0 + row;
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(kAWaves* kWave) void attention_mfma(const AttnArgs 
         float* const s_v = s_kv[buf] + AK * KS;
 #pragma unroll
         for (int j = 0; j < NL; j++) {
-            const int f = threadIdx.x + j * kAWaves * kWave;
+            const int f = threadIdx.x + j * W * kWave;
             const int row = f / (D / 4);
             const int c4 = f - row * (D / 4);
             *reinterpret_cast<float4*>(s_k + row * KS + 4 * c4) = pk[j];
@@ -341,36 +341,41 @@ __global__ __launch_bounds__(kGenWaves* kWave) void attention_generic(const Attn
 }  // namespace
 
 int attention_tuned_dim(int d) { return d == 32 || d == 64 || d == 128 || d == 256; }
-int attention_query_block() { return kAQ; }
 int attention_key_tile(int d) { return d >= 256 ? attention_tile<256>() : attention_tile<128>(); }
 int attention_max_splits(int) { return kAttnMaxSplits; }
 
+namespace {
+template <int D, int W>
+void launch_mfma_attention(const AttnArgs& a, int glog, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((a.M + 16 * W - 1) / (16 * W)), static_cast<unsigned>(a.splits));
+    hipLaunchKernelGGL((attention_mfma<D, W>), grid, dim3(W * kWave), 0, stream, a);
+    if (a.splits > 1) {
+        const dim3 mgrid(static_cast<unsigned>(
+            ((static_cast<long long>(a.M) * (D / 4) << glog) + kMergeThreads - 1) / kMergeThreads));
+        hipLaunchKernelGGL(attention_merge<D>, mgrid, dim3(kMergeThreads), 0, stream, a, glog);
+    }
+}
+template <int D>
+void launch_mfma_attention_d(const AttnArgs& a, int glog, hipStream_t stream) {
+    if constexpr (D <= 128) {  // at d = 256 a 4-wave block would need over 256 VGPRs
+        if (a.qblock == kAttnBlockNarrow) {
+            launch_mfma_attention<D, kAttnBlockNarrow / 16>(a, glog, stream);
+            return;
+        }
+    }
+    launch_mfma_attention<D, kAttnBlockWide / 16>(a, glog, stream);
+}
+}  // namespace
+
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
     if (attention_tuned_dim(a.d)) {
-        const dim3 grid(static_cast<unsigned>((a.M + kAQ - 1) / kAQ), static_cast<unsigned>(a.splits));
-        const dim3 block(kAWaves * kWave);
         int glog = 0;  // lanes per merge group: at most 8 splits per lane, at most a wave
         while (glog < 6 && ((a.splits - 1) >> glog) >= 8) glog++;
-        const dim3 mgrid(static_cast<unsigned>(
-            ((static_cast<long long>(a.M) * (a.d / 4) << glog) + kMergeThreads - 1) / kMergeThreads));
-        const dim3 mblock(kMergeThreads);
         switch (a.d) {
-            case 32:
-                hipLaunchKernelGGL(attention_mfma<32>, grid, block, 0, stream, a);
-                if (a.splits > 1) hipLaunchKernelGGL(attention_merge<32>, mgrid, mblock, 0, stream, a, glog);
-                break;
-            case 64:
-                hipLaunchKernelGGL(attention_mfma<64>, grid, block, 0, stream, a);
-                if (a.splits > 1) hipLaunchKernelGGL(attention_merge<64>, mgrid, mblock, 0, stream, a, glog);
-                break;
-            case 128:
-                hipLaunchKernelGGL(attention_mfma<128>, grid, block, 0, stream, a);
-                if (a.splits > 1) hipLaunchKernelGGL(attention_merge<128>, mgrid, mblock, 0, stream, a, glog);
-                break;
-            default:
-                hipLaunchKernelGGL(attention_mfma<256>, grid, block, 0, stream, a);
-                if (a.splits > 1) hipLaunchKernelGGL(attention_merge<256>, mgrid, mblock, 0, stream, a, glog);
-                break;
+            case 32: launch_mfma_attention_d<32>(a, glog, stream); break;
+            case 64: launch_mfma_attention_d<64>(a, glog, stream); break;
+            case 128: launch_mfma_attention_d<128>(a, glog, stream); break;
+            default: launch_mfma_attention_d<256>(a, glog, stream); break;
         }
         return hipGetLastError();
     }

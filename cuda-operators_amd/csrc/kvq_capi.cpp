@@ -361,6 +361,7 @@ int attention_target_workgroups(int d) { return d >= 128 ? 256 : 512; }
 struct AttnPlan {
     bool tuned = false;
     int splits = 1, chunk = 0;
+    int qblock = kvq::kAttnBlockWide;
     size_t ml_bytes = 0, acc_bytes = 0;
     size_t bytes() const { return ml_bytes + acc_bytes; }
 };
@@ -378,12 +379,22 @@ AttnPlan attention_plan(int M, int N, int d, bool aligned, int requested) {
     p.chunk = N;
     if (!p.tuned) return p;  // the generic kernel runs unsplit
     const int tile = kvq::attention_key_tile(d);
-    const long long qblocks = (static_cast<long long>(M) + kvq::attention_query_block() - 1) /
-                              kvq::attention_query_block();
     const long long tiles = (static_cast<long long>(N) + tile - 1) / tile;
     const long long target = attention_target_workgroups(d);
-    long long want = requested > 0 ? requested : (target + qblocks - 1) / qblocks;
-    want = std::max(1LL, std::min({want, tiles, static_cast<long long>(kvq::attention_max_splits(d))}));
+    // Splits for query blocks of qb: enough to fill the target, in whole key
+    // tiles, within the merge's limit.
+    auto splits_for = [&](int qb) {
+        const long long qblocks = (static_cast<long long>(M) + qb - 1) / qb;
+        const long long w = requested > 0 ? requested : (target + qblocks - 1) / qblocks;
+        return std::max(1LL, std::min({w, tiles, static_cast<long long>(kvq::attention_max_splits(d))}));
+    };
+    long long want = splits_for(kvq::kAttnBlockWide);
+    const long long wide_wgs = (static_cast<long long>(M) + kvq::kAttnBlockWide - 1) / kvq::kAttnBlockWide * want;
+    if (requested == 0 && wide_wgs < target && d <= 128) {
+        // The wide blocks leave CUs idle: narrow blocks double the grid.
+        p.qblock = kvq::kAttnBlockNarrow;
+        want = splits_for(kvq::kAttnBlockNarrow);
+    }
     // The merge runs up to 64 lanes per 16-byte output column, indexed in int.
     if (static_cast<long long>(M) * (d / 4) * 64 >= INT_MAX) want = 1;
     const long long chunk_tiles = (tiles + want - 1) / want;
@@ -412,6 +423,7 @@ hipError_t attention_run(int M, int N, int d, const float* q, const float* k, co
     a.d = d;
     a.splits = p.splits;
     a.chunk = p.chunk;
+    a.qblock = p.qblock;
     a.scale_log2 = scale * 1.4426950408889634f;
     if (p.splits > 1) {
         char* base = static_cast<char*>(ws);

@@ -141,6 +141,12 @@ hipError_t launch_prefill(const PrefillArgs& a, int d, bool bf16, bool vec_ok, h
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 
 // Dense fp32 attention (kvq_attention.hip): out = softmax(q k^T * scale) v.
+// Queries per matrix-core attention workgroup (16 per wave): 8 waves, or 4
+// when the wide blocks times the key splits cannot fill one round of
+// workgroups (few queries, or few keys to split).
+constexpr int kAttnBlockWide = 128;
+constexpr int kAttnBlockNarrow = 64;
+
 struct AttnArgs {
     const float* q;    // [M, d]
     const float* k;    // [N, d]
@@ -150,10 +156,10 @@ struct AttnArgs {
     float* part_acc;   // [splits, M, d] unnormalised partial accumulators
     int M, N, d;
     int splits, chunk;  // key splits (grid y) and keys per split (a multiple of the key tile)
+    int qblock;         // queries per matrix-core workgroup: kAttnBlockWide or kAttnBlockNarrow
     float scale_log2;   // softmax scale * log2(e)
 };
 int attention_tuned_dim(int d);   // the matrix-core kernel handles head dim d
-int attention_query_block();      // queries per matrix-core workgroup
 int attention_key_tile(int d);    // keys per LDS tile of the matrix-core kernel at head dim d
 int attention_max_splits(int d);  // most key splits per matrix-core launch (tuned d)
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);

@@ -41,8 +41,11 @@ def _close(got, ref, what=""):
 
 @pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("M,N", [(1, 1), (1, 4099), (7, 64), (128, 65), (129, 300), (200, 1000), (256, 4096),
-                                 (1000, 127), (513, 2048)])
+                                 (1000, 127), (513, 2048), (63, 1024), (65, 700), (191, 256)])
 def test_attention_online_tuned(o, d, M, N):
+    """Query blocks of 128 (8 waves) where they fill the GPU -- (256, 4096)
+    -- and of 64 (4 waves, d <= 128) where they do not: the other shapes,
+    with rows past M in the last block."""
     rng = np.random.default_rng(M * 7919 + N * 31 + d)
     q, k, v = _problem(rng, M, N, d)
     out = _gpu.poisoned((M, d))
