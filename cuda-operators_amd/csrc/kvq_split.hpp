@@ -216,8 +216,8 @@ __device__ __forceinline__ void store_result(const DecodeArgs& a, const RecMap& 
 }
 
 // Merge of one sequence group's records by a whole workgroup (nheads <=
-// kMergeHeads, nsplit <= kMergeSplits, d % 4 == 0, the group's records below
-// 2 GiB).  Every load is issued with as many others in flight as registers
+// kMergeHeads, nsplit <= kMergeSplits, nheads * nsplit <= 8 per thread, d % 4
+// == 0, the group's records below 2 GiB; merge_group_fits).  Every load is issued with as many others in flight as registers
 // allow, since the merge runs after the rest of the launch has drained and
 // its latency adds directly to the step time:
 // 1. one coherent 8-byte load per (head, split) for (m, l), into LDS;
