@@ -79,12 +79,17 @@ __device__ __forceinline__ int pack_bytes(const int* b) {
 }
 
 // Piece slot of 16-byte piece p of V row rw in an LDS tile (rows of D / 16
-// pieces): the 8 rows one transposed read takes (4g .. 4g+3 and
-// 16+4g .. 16+4g+3) land in 8 different 16-byte bank groups.
+// pieces).  LDS serves 256 bytes (64 banks of 4 bytes) per cycle, and a
+// transposed read takes 32 lanes per cycle: 16 rows (4g .. 4g+3 and
+// 16+4g .. 16+4g+3 for the two 16-lane groups g of the half wave) of 16
+// bytes each.  A row's 16-byte bank group is (row bytes / 16 * rw + slot)
+// mod 16, so rows that share a bank half (D = 128: equal parity; D = 64:
+// equal rw mod 4) must get distinct slots.  Tile stores write whole rows, so
+// any per-row permutation keeps them conflict-free.
 template <int D>
 __device__ __forceinline__ int v_slot(int p, int rw) {
-    if constexpr (D == 128) return p ^ (rw & 7);
-    else return p ^ (((rw >> 1) & 1) | ((rw >> 3) & 2));
+    if constexpr (D == 128) return p ^ (((rw >> 1) & 3) | ((rw >> 2) & 4));
+    else return p ^ (((rw >> 2) & 1) | ((rw >> 3) & 2));
 }
 
 template <int D, int G, bool PAGED, bool FIT>
@@ -97,10 +102,12 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     constexpr int RPLV = kWave / NB;      // V rows one tile load instruction covers
     constexpr int NV = kMTile / RPLV;     // V load instructions per tile
     constexpr int NE = 2 * D / kWave;     // appended K+V elements per lane of the owning wave
-    // V tile buffers during the tile loop; the waves' results afterwards.
+    // V tile buffers during the tile loop; the waves' results afterwards
+    // (rows padded by one float, so the lanes of one result column, 16 rows
+    // apart, hit different banks).
     union TileOrResult {
         int8_t v[kMWaves][2][kMTile * D];
-        float acc[kMWaves][16][D];
+        float acc[kMWaves][16][D + 1];
     };
     __shared__ __align__(16) TileOrResult s_u;
     auto& s_v = s_u.v;
@@ -316,8 +323,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         }
     };
     // V rows into an LDS tile buffer: 16-byte piece p of row rw is stored at
-    // piece p ^ (rw & 7), so the transposed reads of 8 rows hit 8 different
-    // bank groups.
+    // slot v_slot(p, rw), which keeps the transposed reads conflict-free.
     auto stage_v = [&](const Tile& T, int8_t* vt) {
 #pragma unroll
         for (int c = 0; c < NV; c++) {
