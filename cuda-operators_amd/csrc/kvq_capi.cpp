@@ -139,7 +139,8 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
         const size_t recs = static_cast<size_t>(p.sched_items) * Hq;
         p.counter_bytes = kCounterBytes;
         p.sched_bytes =
-            round_up((kvq::kSchedHeader + 2 * static_cast<size_t>(p.sched_items) + 2 * static_cast<size_t>(B)) *
+            round_up((kvq::kSchedHeader + kvq::kSchedItemInts * static_cast<size_t>(p.sched_items) +
+                      2 * static_cast<size_t>(B)) *
                          sizeof(int),
                      kAlign);
         p.ml_bytes = round_up(recs * 2 * sizeof(float), kAlign);

@@ -357,8 +357,7 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     // Merge the waves; one thread per (head, element).
     RecMap map{0, 0, 0};
     if (nsplit > 1) {
-        if constexpr (FIT) map = rec_map_fit(a, w, bhq0);
-        else map = rec_map(a, b, bhq0);
+        map = rec_map(a, w, bhq0);
     }
     for (int i = threadIdx.x; i < SG * D; i += blockDim.x) {
         const int h = i / D;
@@ -385,7 +384,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a) {
     const int len = seq_len_of(a, b);
     const int nsplit = (len + a.chunk - 1) / a.chunk;
     if (nsplit <= 1) return;  // written directly by the decode kernel
-    const RecMap map = rec_map(a, b, bhq);
+    const RecMap map = rec_map_static(a, bhq);
     for (int dim = threadIdx.x; dim < a.d; dim += blockDim.x)
         a.out[static_cast<size_t>(bhq) * a.d + dim] = merge_dim(a, map, 0, dim, nsplit);
 }

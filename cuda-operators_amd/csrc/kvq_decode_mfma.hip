@@ -494,8 +494,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // Merge the waves and the hi/lo rows; one thread per (head, element).
     RecMap map{0, 0, 0};
     if (nsplit > 1) {
-        if constexpr (FIT) map = rec_map_fit(a, w, bhq0);
-        else map = rec_map(a, b, bhq0);
+        map = rec_map(a, w, bhq0);
     }
     for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
         const int h = i / D;

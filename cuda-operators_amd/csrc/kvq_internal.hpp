@@ -60,15 +60,19 @@ struct DecodeArgs {
 // Split schedule of a ragged batch, computed on the device from the lengths
 // by schedule_kernel before the decode launch (int words):
 //   [0] chunk: the largest tokens per split;  [1] item count;  [2], [3] unused
-//   items  [kSchedHeader, + 2 * sched_items): (batch index, split index) per
-//          work item, every split of every sequence once (a length-0
-//          sequence has one empty item that writes its zero output);
-//   seq [B] int2 after the items: (rec_base, chunk) of sequence b: its split
-//          s covers tokens [s * chunk, (s + 1) * chunk) and owns records
-//          (rec_base + s) * Hq + hq.
+//   items  [kSchedHeader, + kSchedItemInts * sched_items): per work item
+//          (batch index b, split index s, splits of b, first record of b,
+//          chunk of b, length of b, 0, 0) -- everything a decode workgroup
+//          needs in two 16-byte loads; every split of every sequence once
+//          (a length-0 sequence has one empty item that writes its zero
+//          output).  Split s covers tokens [s * chunk, (s + 1) * chunk) and
+//          owns records (first record + s) * Hq + hq;
+//   seq [B] int2 after the items: (first record, chunk) of sequence b, for
+//          the schedule kernel's own passes.
 // Workgroup i of the decode grid takes item i / U, work unit i % U of that
 // sequence (U = Hkv * nsg).
 constexpr int kSchedHeader = 4;
+constexpr int kSchedItemInts = 8;
 
 // Most sequences of a ragged batch the matrix-core kernel plans itself (one
 // per lane of a wave).

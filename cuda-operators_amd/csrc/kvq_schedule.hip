@@ -69,6 +69,14 @@ __device__ __forceinline__ int clamped_len(const int32_t* lengths, int b, int ma
     return min(max(lengths[b], 0), max_len);
 }
 
+// Work item pos: split s of sequence b (n splits of chunk tokens, first
+// record rec, len tokens), in the layout at kSchedHeader (kvq_internal.hpp).
+__device__ __forceinline__ void put_item(int* items, int pos, int b, int s, int n, int rec, int chunk, int len) {
+    int4* it = reinterpret_cast<int4*>(items + kSchedItemInts * pos);
+    it[0] = make_int4(b, s, n, rec);
+    it[1] = make_int4(chunk, len, 0, 0);
+}
+
 __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* lengths, int B, int max_len,
                                                                  int units, int target, int gran, int items_cap,
                                                                  int* sched) {
@@ -101,7 +109,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
     for (int w = 0; w < kSchedWaves; w++) total += s_sum[w];
 
     int* items = sched + kSchedHeader;
-    int2* seq = reinterpret_cast<int2*>(items + 2 * items_cap);  // (rec_base, chunk) per sequence
+    int2* seq = reinterpret_cast<int2*>(items + kSchedItemInts * items_cap);  // (rec_base, chunk) per sequence
     const long long cmax = (static_cast<long long>(max(max_len, 1)) + gran - 1) / gran * gran;
     const int S = target / units;
 
@@ -128,10 +136,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
         if (t < B) {
             seq[t] = make_int2(pre, cb);
             for (int s = 0; s < n; s++) {
-                if (pre + s < items_cap) {
-                    items[2 * (pre + s)] = t;
-                    items[2 * (pre + s) + 1] = s;
-                }
+                if (pre + s < items_cap) put_item(items, pre + s, t, s, n, pre, cb, s_len[t]);
             }
         }
         if (t == 0) {
@@ -160,10 +165,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
             seq[b] = make_int2(rec_carry + pre_n, chunk);
             for (int s = 0; s < full; s++) {
                 const int pos = full_carry + pre_f + s;
-                if (pos < items_cap) {
-                    items[2 * pos] = b;
-                    items[2 * pos + 1] = s;
-                }
+                if (pos < items_cap) put_item(items, pos, b, s, n, rec_carry + pre_n, chunk, len);
             }
             const int last = len - (n - 1) * chunk;  // in [0, chunk]
             const int cls = static_cast<int>(static_cast<long long>(chunk - last) * kSizeClasses / (chunk + 1));
@@ -191,10 +193,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
         const int last = len - (n - 1) * chunk;
         const int cls = static_cast<int>(static_cast<long long>(chunk - last) * kSizeClasses / (chunk + 1));
         const int pos = atomicAdd(&s_class[cls], 1);
-        if (pos < items_cap) {
-            items[2 * pos] = b;
-            items[2 * pos + 1] = n - 1;
-        }
+        if (pos < items_cap) put_item(items, pos, b, n - 1, n, seq[b].x, chunk, len);
     }
     if (t == 0) {
         sched[0] = chunk;

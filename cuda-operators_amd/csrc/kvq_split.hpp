@@ -32,21 +32,30 @@ __device__ __forceinline__ bool locate_work(const DecodeArgs& a, SplitWork& w) {
     const int U = a.Hkv * a.nsg;
     int chunk;
     if (a.sched) {
+        // The count and the item (in bounds: the grid has sched_items items)
+        // load together, one round trip before the workgroup's first tile.
         const int item = blockIdx.x / U;
-        if (item >= a.sched[1]) return false;
-        w.b = a.sched[kSchedHeader + 2 * item];
-        w.split = a.sched[kSchedHeader + 2 * item + 1];
+        const int count = a.sched[1];
+        const int4* it = reinterpret_cast<const int4*>(a.sched + kSchedHeader + kSchedItemInts * item);
+        const int4 i0 = it[0];
+        const int4 i1 = it[1];
+        if (item >= count) return false;
+        w.b = i0.x;
+        w.split = i0.y;
+        w.nsplit = i0.z;
+        w.rec = i0.w;
+        chunk = i1.x;
+        w.len = i1.y;
         w.unit = w.b * U + (blockIdx.x - item * U);
-        chunk = a.sched[kSchedHeader + 2 * a.sched_items + 2 * w.b + 1];
     } else {
         const int units = a.B * U;
         w.split = blockIdx.x / units;
         w.unit = blockIdx.x - w.split * units;
         w.b = w.unit / U;
         chunk = a.chunk;
+        w.len = seq_len_of(a, w.b);
+        w.nsplit = w.len == 0 ? 1 : (w.len + chunk - 1) / chunk;
     }
-    w.len = seq_len_of(a, w.b);
-    w.nsplit = w.len == 0 ? 1 : (w.len + chunk - 1) / chunk;
     if (w.split >= w.nsplit) return false;
     w.t0 = w.split * chunk;
     w.t1 = min(w.len, w.t0 + chunk);
@@ -134,19 +143,18 @@ struct RecMap {
     int hs, ss;
 };
 
-__device__ __forceinline__ RecMap rec_map(const DecodeArgs& a, int b, size_t bhq0) {
-    if (a.fit_items > 0) return {0, 0, 0};  // callers under an in-kernel plan use rec_map_fit
-    if (a.sched) {
-        const int base = a.sched[kSchedHeader + 2 * a.sched_items + 2 * b];
-        return {static_cast<size_t>(base) * a.Hq + (bhq0 - static_cast<size_t>(b) * a.Hq), 1, a.Hq};
-    }
+// Records of static splits: [B, Hq, splits].
+__device__ __forceinline__ RecMap rec_map_static(const DecodeArgs& a, size_t bhq0) {
     return {bhq0 * a.splits, a.splits, 1};
 }
 
-// Records of an in-kernel plan (locate_fit): sequence b's split s owns
-// records (rec + s) * Hq + hq.
-__device__ __forceinline__ RecMap rec_map_fit(const DecodeArgs& a, const SplitWork& w, size_t bhq0) {
-    return {static_cast<size_t>(w.rec) * a.Hq + (bhq0 - static_cast<size_t>(w.b) * a.Hq), 1, a.Hq};
+// Records of workgroup w's sequence: under the in-kernel plan (locate_fit) or
+// the split schedule, split s of sequence b owns records (w.rec + s) * Hq + hq;
+// otherwise static splits.
+__device__ __forceinline__ RecMap rec_map(const DecodeArgs& a, const SplitWork& w, size_t bhq0) {
+    if (a.fit_items > 0 || a.sched)
+        return {static_cast<size_t>(w.rec) * a.Hq + (bhq0 - static_cast<size_t>(w.b) * a.Hq), 1, a.Hq};
+    return rec_map_static(a, bhq0);
 }
 
 // U consecutive per-token scales (U in {1,2,4,8}); p is U*4-byte aligned when

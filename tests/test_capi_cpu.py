@@ -162,7 +162,7 @@ def test_matrix_core_plan_by_workspace(L, B):
         assert n == 256 * 1024 + _ru(items * Hq * 2 * 4) + _ru(items * Hq * d * 4)
     else:
         items = B + (512 + Hkv - 1) // Hkv + 1
-        sched = _ru((4 + 2 * items + 2 * B) * 4)
+        sched = _ru((4 + 8 * items + 2 * B) * 4)
         assert n == 256 * 1024 + sched + _ru(items * Hq * 2 * 4) + _ru(items * Hq * d * 4)
 
 
