@@ -512,7 +512,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         }
         store_result(a, map, bhq0, h, dim, split, nsplit, M, L, A);
     }
-    finish_split(a, unit, map, bhq0, G, nsplit, &s_last);
+    finish_split<true>(a, unit, map, bhq0, G, nsplit, &s_last);
 }
 
 }  // namespace

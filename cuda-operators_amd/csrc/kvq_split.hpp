@@ -350,9 +350,62 @@ __device__ inline void merge_group(const DecodeArgs& a, const RecMap& map, size_
     }
 }
 
+// Merge of at most kFlatSplits splits in one round trip: one thread per
+// (head, 16-byte output column) loads that head's (m, l) and its accumulator
+// column of every split together, then combines them in registers -- no LDS,
+// no barrier, against merge_group's two load phases and three barriers (cfg2:
+// 36.6 -> 34.1 us).  Same conditions as merge_group otherwise.
+constexpr int kFlatSplits = 16;
+
+__device__ inline void merge_flat(const DecodeArgs& a, const RecMap& map, size_t bhq0, int nheads, int nsplit) {
+    const int d = a.d;
+    const int cpr = d >> 2;
+    const unsigned span = static_cast<unsigned>(merge_span(map, nheads, nsplit));
+    const buf_rsrc mlr = make_rsrc(a.part_ml + map.r0 * 2, span * 8u);
+    const buf_rsrc accr = make_rsrc(a.part_acc + map.r0 * d, span * static_cast<unsigned>(d) * 4u);
+    typedef int v2i_t __attribute__((ext_vector_type(2)));
+    for (int c = threadIdx.x; c < nheads * cpr; c += blockDim.x) {
+        const int h = c / cpr;
+        const int col = c - h * cpr;
+        v2i_t ml[kFlatSplits];
+        v4i_t acc[kFlatSplits];
+#pragma unroll
+        for (int k = 0; k < kFlatSplits; k++) {
+            const int rec = h * map.hs + k * map.ss;
+            if (k < nsplit) {
+                ml[k] = __builtin_amdgcn_raw_buffer_load_b64(mlr, rec * 8, 0, kCoherent);
+                acc[k] = __builtin_amdgcn_raw_buffer_load_b128(accr, (rec * d + 4 * col) * 4, 0, kCoherent);
+            }
+        }
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < kFlatSplits; k++)
+            if (k < nsplit) M = fmaxf(M, __int_as_float(ml[k].x));
+        const float Ms = M == -INFINITY ? 0.0f : M;
+        float L = 0.0f;
+        float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int k = 0; k < kFlatSplits; k++) {
+            if (k < nsplit) {
+                const float w = fast_exp2(__int_as_float(ml[k].x) - Ms);
+                L = fmaf(__int_as_float(ml[k].y), w, L);
+                A.x = fmaf(__int_as_float(acc[k].x), w, A.x);
+                A.y = fmaf(__int_as_float(acc[k].y), w, A.y);
+                A.z = fmaf(__int_as_float(acc[k].z), w, A.z);
+                A.w = fmaf(__int_as_float(acc[k].w), w, A.w);
+            }
+        }
+        float* o = a.out + (bhq0 + h) * d + 4 * col;
+        o[0] = A.x / L, o[1] = A.y / L, o[2] = A.z / L, o[3] = A.w / L;
+    }
+}
+
 // Called by every thread of a workgroup after its store_result calls: counts
 // the split's arrival and, in the last workgroup of the work unit, merges the
-// records of rows [bhq0, bhq0 + nheads).  s_last: one int of LDS.
+// records of rows [bhq0, bhq0 + nheads).  s_last: one int of LDS.  FLAT: up
+// to kFlatSplits splits merge with merge_flat (its registers are not worth
+// taking from the FMA kernel, whose ragged batches rarely split).
+template <bool FLAT = false>
 __device__ __forceinline__ void finish_split(const DecodeArgs& a, int unit, const RecMap& map, size_t bhq0,
                                              int nheads, int nsplit, int* s_last) {
     if (nsplit <= 1 || a.counters == nullptr) return;
@@ -364,7 +417,9 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, int unit, cons
     }
     __syncthreads();
     if (*s_last) {
-        if (merge_group_fits(a, map, nheads, nsplit)) {
+        if (FLAT && nsplit <= kFlatSplits && merge_group_fits(a, map, nheads, nsplit)) {
+            merge_flat(a, map, bhq0, nheads, nsplit);
+        } else if (merge_group_fits(a, map, nheads, nsplit)) {
             merge_group(a, map, bhq0, nheads, nsplit);
         } else {
             for (int i = threadIdx.x; i < nheads * a.d; i += blockDim.x) {
