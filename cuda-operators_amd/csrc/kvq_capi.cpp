@@ -245,7 +245,9 @@ hipError_t reference_launch(const float* Q, const int8_t* K, const int8_t* V, co
 
 // Library-owned, per-device split workspace for the legacy `solve` ABI.  Grown
 // on demand (hipFree waits for in-flight work) and zero-filled on allocation;
-// completed launches leave the arrival counters at zero.
+// completed launches leave the arrival counters at zero.  `launch(ptr)` is
+// enqueued while the lock is held, so a concurrent call that grows the
+// workspace frees it only after this launch is on the null stream.
 struct SolveWorkspace {
     void* ptr = nullptr;
     size_t bytes = 0;
@@ -253,9 +255,9 @@ struct SolveWorkspace {
 std::mutex g_ws_mutex;
 SolveWorkspace g_ws[64];
 
-hipError_t solve_workspace(size_t need, void** out) {
-    *out = nullptr;
-    if (need == 0) return hipSuccess;
+template <class Launch>
+hipError_t with_solve_workspace(size_t need, Launch&& launch) {
+    if (need == 0) return launch(nullptr);
     int dev = 0;
     hipError_t err = hipGetDevice(&dev);
     if (err != hipSuccess) return err;
@@ -276,8 +278,7 @@ hipError_t solve_workspace(size_t need, void** out) {
         if (err != hipSuccess) return err;
         w.bytes = bytes;
     }
-    *out = w.ptr;
-    return hipSuccess;
+    return launch(w.ptr);
 }
 
 bool decode_params_ok(const kvq_decode_params* p) {
@@ -437,7 +438,9 @@ hipError_t attention_run(int M, int N, int d, const float* q, const float* k, co
 // Library-owned attention workspaces, one per (device, stream): launches on
 // one stream are ordered and may share one; different streams must not.
 // Grown on demand (hipFree waits for in-flight work); the split records need
-// no initial contents.
+// no initial contents.  As for `solve`, `launch(ptr)` is enqueued under the
+// lock, so a concurrent call on the same stream cannot free the workspace
+// before this launch exists.
 struct AttnWorkspaceKey {
     int device;
     hipStream_t stream;
@@ -448,9 +451,9 @@ struct AttnWorkspaceKey {
 std::mutex g_attn_ws_mutex;
 std::map<AttnWorkspaceKey, SolveWorkspace> g_attn_ws;
 
-hipError_t attention_workspace(size_t need, hipStream_t stream, void** out) {
-    *out = nullptr;
-    if (need == 0) return hipSuccess;
+template <class Launch>
+hipError_t with_attention_workspace(size_t need, hipStream_t stream, Launch&& launch) {
+    if (need == 0) return launch(nullptr);
     int dev = 0;
     hipError_t err = hipGetDevice(&dev);
     if (err != hipSuccess) return err;
@@ -468,8 +471,7 @@ hipError_t attention_workspace(size_t need, hipStream_t stream, void** out) {
         if (err != hipSuccess) return err;
         w.bytes = bytes;
     }
-    *out = w.ptr;
-    return hipSuccess;
+    return launch(w.ptr);
 }
 
 }  // namespace
@@ -495,12 +497,10 @@ void solve(const float* Q, const int8_t* K_int8, const int8_t* V_int8, const flo
     a.splits = p.splits;
     a.chunk = p.chunk;
     a.nsg = p.nsg;
-    void* ws = nullptr;
-    hipError_t err = solve_workspace(plan_bytes(p), &ws);
-    if (err == hipSuccess) {
+    const hipError_t err = with_solve_workspace(plan_bytes(p), [&](void* ws) {
         bind_workspace(a, p, ws);
-        err = kvq::launch_decode(a, p, nullptr);
-    }
+        return kvq::launch_decode(a, p, nullptr);
+    });
     if (err != hipSuccess) fprintf(stderr, "[kvq] solve: HIP error: %s (%s)\n", hipGetErrorName(err), hipGetErrorString(err));
 }
 
@@ -692,10 +692,9 @@ hipError_t attention_online_launch(const float* Q, const float* K, const float* 
                                    int d, hipStream_t stream) {
     if (!attention_args_ok(M, N, d, Q, K, V, output)) return hipErrorInvalidValue;
     const AttnPlan p = attention_plan(M, N, d, attention_aligned(Q, K, V, output), 0);
-    void* ws = nullptr;
-    const hipError_t err = attention_workspace(p.bytes(), stream, &ws);
-    if (err != hipSuccess) return err;
-    return attention_run(M, N, d, Q, K, V, output, 1.0f / sqrtf(static_cast<float>(d)), p, ws, stream);
+    return with_attention_workspace(p.bytes(), stream, [&](void* ws) {
+        return attention_run(M, N, d, Q, K, V, output, 1.0f / sqrtf(static_cast<float>(d)), p, ws, stream);
+    });
 }
 
 size_t kvq_attention_workspace_size(const kvq_attention_params* p) {
