@@ -293,6 +293,202 @@ __global__ __launch_bounds__(W* kWave) void attention_mfma(const AttnArgs a) {
     }
 }
 
+// attention_rows<D, QM>: up to QM <= 8 queries (decode-shaped attention) on
+// the VALU, with no LDS tiles and no padded query block.  A key row is held by
+// a group of L lanes, each with E = D/L of its dims: float4 number j·L + lane
+// of the row, for j < E/4, so each load instruction reads 16·L contiguous
+// bytes per group.  A wave covers 64/L keys per load and keeps 4 loads of K
+// and 4 of V in flight per lane (8 KB per wave at any D), so a workgroup step
+// is 4096/D keys whatever L is.  Each key group keeps its own online-softmax
+// state per query; its scores are sums over the group's lanes (DPP within a
+// 16-lane row, ds_bpermute across rows).  L = D/4 (4 dims per lane), except
+// 16 at d = 128 with 4-8 queries: there the per-key cross-row sums dominated
+// the ALU time (M = 8, N = 65536: 31.7 -> 23.4 us); with fewer queries, or at
+// d = 256 (16 dims per lane, one key per lane and step), 4 dims per lane ran
+// faster.  The epilogue merges the groups of a wave (shuffles), then the waves
+// (LDS), and writes the output, or the split's (m, l, acc) record for
+// attention_merge.
+constexpr int kRowsWaves = 4;
+constexpr int kRowsLoads = 4;  // float4 loads of K (and of V) in flight per lane
+constexpr int kRowsMaxQueries = 8;
+template <int D, int QM>
+struct RowsShape {
+    static constexpr int L = D == 128 && QM >= 4 ? 16 : D / 4;  // lanes per key row
+    static constexpr int E = D / L;                              // dims per lane
+    static constexpr int NV = E / 4;                             // float4 loads per row per lane
+    static constexpr int U = kRowsLoads / NV;                    // keys per lane per step
+    static constexpr int KW = kWave / L;                         // keys per wave load
+    static constexpr int T = kRowsWaves * KW * U;                // keys per workgroup step
+    static_assert(T == 4096 / D, "a workgroup step is 4096/D keys at any group width");
+};
+template <int D>
+constexpr int rows_tile() {
+    return RowsShape<D, 1>::T;
+}
+
+template <int L>
+__device__ __forceinline__ float key_sum(float x) {
+    if constexpr (L <= 16) {
+        return group_sum<L>(x);
+    } else {
+        x = group_sum<16>(x);
+        x += __shfl_xor(x, 16);
+        if constexpr (L == 64) x += __shfl_xor(x, 32);
+        return x;
+    }
+}
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 load_row16(const float* p) {
+    const f32x4v t = __builtin_nontemporal_load(reinterpret_cast<const f32x4v*>(p));
+    return make_float4(t.x, t.y, t.z, t.w);
+}
+
+template <int D, int QM>
+__global__ __launch_bounds__(kRowsWaves* kWave) void attention_rows(const AttnArgs a) {
+    using S = RowsShape<D, QM>;
+    constexpr int L = S::L, E = S::E, NV = S::NV, U = S::U, KW = S::KW, T = S::T;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int kg = lane / L;
+    const int ds = lane % L;
+    const int q0 = blockIdx.x * QM;
+    const int split = blockIdx.y;
+    const int k0 = split * a.chunk;
+    const int k1 = min(a.N, k0 + a.chunk);
+
+    // Element 4j + i of a lane's dims is dim 4(jL + ds) + i.
+    float qv[QM][E], acc[QM][E], m[QM], l[QM];
+#pragma unroll
+    for (int qi = 0; qi < QM; qi++) {
+        const int q = q0 + qi;
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const float4 x = q < a.M ? *reinterpret_cast<const float4*>(a.q + static_cast<size_t>(q) * D + 4 * (j * L + ds))
+                                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            qv[qi][4 * j] = x.x * a.scale_log2;
+            qv[qi][4 * j + 1] = x.y * a.scale_log2;
+            qv[qi][4 * j + 2] = x.z * a.scale_log2;
+            qv[qi][4 * j + 3] = x.w * a.scale_log2;
+        }
+        m[qi] = -INFINITY;
+        l[qi] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; e++) acc[qi][e] = 0.0f;
+    }
+
+    for (int base = k0 + wave * KW * U; base < k1; base += T) {
+        float kr[U][E], vr[U][E];
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int t = base + u * KW + kg;
+            ok[u] = t < k1;
+            const size_t row = static_cast<size_t>(ok[u] ? t : k1 - 1) * D + 4 * ds;
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                const float4 x = load_row16(a.k + row + 4 * L * j);
+                const float4 y = load_row16(a.v + row + 4 * L * j);
+                kr[u][4 * j] = x.x; kr[u][4 * j + 1] = x.y; kr[u][4 * j + 2] = x.z; kr[u][4 * j + 3] = x.w;
+                vr[u][4 * j] = y.x; vr[u][4 * j + 1] = y.y; vr[u][4 * j + 2] = y.z; vr[u][4 * j + 3] = y.w;
+            }
+        }
+#pragma unroll
+        for (int qi = 0; qi < QM; qi++) {
+            float s[U];
+            float mx = m[qi];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                float dot = qv[qi][0] * kr[u][0];
+#pragma unroll
+                for (int e = 1; e < E; e++) dot = fmaf(qv[qi][e], kr[u][e], dot);
+                s[u] = key_sum<L>(dot);
+                if (ok[u]) mx = fmaxf(mx, s[u]);
+            }
+            // mx stays -inf only while the group has seen no key; then every
+            // weight below is 0 and the state is unchanged.
+            const float c = mx == m[qi] ? 1.0f : fast_exp2(m[qi] - mx);
+            l[qi] *= c;
+#pragma unroll
+            for (int e = 0; e < E; e++) acc[qi][e] *= c;
+            m[qi] = mx;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const float pw = ok[u] ? fast_exp2(s[u] - mx) : 0.0f;
+                l[qi] += pw;
+#pragma unroll
+                for (int e = 0; e < E; e++) acc[qi][e] = fmaf(pw, vr[u][e], acc[qi][e]);
+            }
+        }
+    }
+
+    // The wave's key groups: lanes ds of every group hold the same dims.
+#pragma unroll
+    for (int qi = 0; qi < QM; qi++) {
+        float mw = m[qi];
+#pragma unroll
+        for (int off = L; off < kWave; off <<= 1) mw = fmaxf(mw, __shfl_xor(mw, off));
+        const float c = m[qi] == -INFINITY ? 0.0f : fast_exp2(m[qi] - mw);
+        l[qi] *= c;
+#pragma unroll
+        for (int e = 0; e < E; e++) acc[qi][e] *= c;
+#pragma unroll
+        for (int off = L; off < kWave; off <<= 1) {
+            l[qi] += __shfl_xor(l[qi], off);
+#pragma unroll
+            for (int e = 0; e < E; e++) acc[qi][e] += __shfl_xor(acc[qi][e], off);
+        }
+        m[qi] = mw;
+    }
+
+    // The workgroup's waves, through LDS (float4 column c4 = jL + ds).
+    __shared__ float2 s_ml[kRowsWaves][QM];
+    __shared__ float4 s_acc[kRowsWaves][QM][D / 4];
+    if (kg == 0) {
+#pragma unroll
+        for (int qi = 0; qi < QM; qi++) {
+#pragma unroll
+            for (int j = 0; j < NV; j++)
+                s_acc[wave][qi][j * L + ds] =
+                    make_float4(acc[qi][4 * j], acc[qi][4 * j + 1], acc[qi][4 * j + 2], acc[qi][4 * j + 3]);
+            if (ds == 0) s_ml[wave][qi] = make_float2(m[qi], l[qi]);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < QM * (D / 4); i += kRowsWaves * kWave) {
+        const int qi = i / (D / 4);
+        const int c4 = i - qi * (D / 4);
+        const int q = q0 + qi;
+        if (q >= a.M) continue;
+        float mm = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kRowsWaves; w++) mm = fmaxf(mm, s_ml[w][qi].x);
+        float ls = 0.0f;
+        float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int w = 0; w < kRowsWaves; w++) {
+            const float2 ml = s_ml[w][qi];
+            const float c = ml.x == -INFINITY ? 0.0f : fast_exp2(ml.x - mm);
+            const float4 x = s_acc[w][qi][c4];
+            ls = fmaf(c, ml.y, ls);
+            A.x = fmaf(c, x.x, A.x);
+            A.y = fmaf(c, x.y, A.y);
+            A.z = fmaf(c, x.z, A.z);
+            A.w = fmaf(c, x.w, A.w);
+        }
+        if (a.splits == 1) {
+            const float inv = 1.0f / ls;
+            *reinterpret_cast<float4*>(a.out + static_cast<size_t>(q) * D + 4 * c4) =
+                make_float4(A.x * inv, A.y * inv, A.z * inv, A.w * inv);
+        } else {
+            const size_t rec = static_cast<size_t>(split) * a.M + q;
+            *reinterpret_cast<float4*>(a.part_acc + rec * D + 4 * c4) = A;
+            if (c4 == 0) *reinterpret_cast<float2*>(a.part_ml + rec * 2) = make_float2(mm, ls);
+        }
+    }
+}
+
 // Any d <= 1024: one wave per query row; scores of 64 keys per step, one per
 // lane (dot over d), online softmax over the steps, accumulator in LDS.
 constexpr int kGenWaves = 4;
@@ -343,6 +539,20 @@ __global__ __launch_bounds__(kGenWaves* kWave) void attention_generic(const Attn
 int attention_tuned_dim(int d) { return d == 32 || d == 64 || d == 128 || d == 256; }
 int attention_key_tile(int d) { return d >= 256 ? attention_tile<256>() : attention_tile<128>(); }
 int attention_max_splits(int) { return kAttnMaxSplits; }
+int attention_rows_queries(int M) {
+    if (M <= 1) return 1;
+    if (M <= 2) return 2;
+    if (M <= 4) return 4;
+    return M <= kRowsMaxQueries ? kRowsMaxQueries : 0;
+}
+int attention_rows_tile(int d) {
+    switch (d) {
+        case 32: return rows_tile<32>();
+        case 64: return rows_tile<64>();
+        case 128: return rows_tile<128>();
+        default: return rows_tile<256>();
+    }
+}
 
 namespace {
 template <int D, int W>
@@ -355,8 +565,31 @@ void launch_mfma_attention(const AttnArgs& a, int glog, hipStream_t stream) {
         hipLaunchKernelGGL(attention_merge<D>, mgrid, dim3(kMergeThreads), 0, stream, a, glog);
     }
 }
+template <int D, int QM>
+void launch_rows_attention(const AttnArgs& a, int glog, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((a.M + QM - 1) / QM), static_cast<unsigned>(a.splits));
+    hipLaunchKernelGGL((attention_rows<D, QM>), grid, dim3(kRowsWaves * kWave), 0, stream, a);
+    if (a.splits > 1) {
+        const dim3 mgrid(static_cast<unsigned>(
+            ((static_cast<long long>(a.M) * (D / 4) << glog) + kMergeThreads - 1) / kMergeThreads));
+        hipLaunchKernelGGL(attention_merge<D>, mgrid, dim3(kMergeThreads), 0, stream, a, glog);
+    }
+}
+template <int D>
+void launch_rows_attention_d(const AttnArgs& a, int glog, hipStream_t stream) {
+    switch (a.qblock) {
+        case 1: launch_rows_attention<D, 1>(a, glog, stream); break;
+        case 2: launch_rows_attention<D, 2>(a, glog, stream); break;
+        case 4: launch_rows_attention<D, 4>(a, glog, stream); break;
+        default: launch_rows_attention<D, kRowsMaxQueries>(a, glog, stream); break;
+    }
+}
 template <int D>
 void launch_mfma_attention_d(const AttnArgs& a, int glog, hipStream_t stream) {
+    if (a.qblock <= kRowsMaxQueries) {
+        launch_rows_attention_d<D>(a, glog, stream);
+        return;
+    }
     if constexpr (D <= 128) {  // at d = 256 a 4-wave block would need over 256 VGPRs
         if (a.qblock == kAttnBlockNarrow) {
             launch_mfma_attention<D, kAttnBlockNarrow / 16>(a, glog, stream);

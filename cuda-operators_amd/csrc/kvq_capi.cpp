@@ -58,6 +58,13 @@ constexpr long kMinSplitUnitBytes = 192 * 1024;
 #ifndef KVQ_FIT_TARGET_VALU
 #define KVQ_FIT_TARGET_VALU 512
 #endif
+// Workgroups of the few-query attention kernel: one 4-wave workgroup per CU
+// streams best for one query (M = 1, N = 65536, d = 128: 15.6 us at 256,
+// 17.0 at 512), two per CU hide the ALU work of more (M = 2: 21.1 us at 256;
+// M = 8: 44.5 us at 256, 31.4 at 512, 37.3 at 1024).
+#ifndef KVQ_ATTN_ROWS_TARGET
+#define KVQ_ATTN_ROWS_TARGET(qm) ((qm) <= 1 ? 256 : 512)
+#endif
 #ifndef KVQ_FIT_TARGET_MFMA
 #define KVQ_FIT_TARGET_MFMA 256
 #endif
@@ -380,6 +387,23 @@ AttnPlan attention_plan(int M, int N, int d, bool aligned, int requested) {
     p.tuned = kvq::attention_tuned_dim(d) && aligned;
     p.chunk = N;
     if (!p.tuned) return p;  // the generic kernel runs unsplit
+    if (const int qm = kvq::attention_rows_queries(M); qm > 0) {
+        // A few queries: the VALU kernel, one query block, key splits to
+        // fill KVQ_ATTN_ROWS_TARGET(qm) workgroups.
+        p.qblock = qm;
+        const long long rt = kvq::attention_rows_tile(d);
+        const long long rtiles = (static_cast<long long>(N) + rt - 1) / rt;
+        const long long want = std::max(1LL, std::min({requested > 0 ? static_cast<long long>(requested)
+                                                                     : static_cast<long long>(KVQ_ATTN_ROWS_TARGET(qm)),
+                                                      rtiles, static_cast<long long>(kvq::attention_max_splits(d))}));
+        p.chunk = static_cast<int>(std::min<long long>((rtiles + want - 1) / want * rt, N));
+        p.splits = static_cast<int>((N + static_cast<long long>(p.chunk) - 1) / p.chunk);
+        if (p.splits > 1) {
+            p.ml_bytes = round_up(static_cast<size_t>(p.splits) * M * 2 * sizeof(float), kAlign);
+            p.acc_bytes = round_up(static_cast<size_t>(p.splits) * M * d * sizeof(float), kAlign);
+        }
+        return p;
+    }
     const int tile = kvq::attention_key_tile(d);
     const long long tiles = (static_cast<long long>(N) + tile - 1) / tile;
     const long long target = attention_target_workgroups(d);

@@ -276,6 +276,13 @@ def test_attention_workspace_plan(L):
     assert size(128, 64, 128) == 0  # one key tile: nothing to split
     # A requested split count is clamped to whole key tiles.
     assert size(128, 8192, 64, splits=1 << 20) == size(128, 8192, 64, splits=8192 // 64) > 0
+    # Up to 8 queries: the few-query kernel splits the keys in its own steps
+    # (4096 / d keys per workgroup step): 256 splits for one query, 512 for more.
+    assert size(1, 65536, 128) >= 256 * (128 + 2) * 4
+    assert size(8, 65536, 128) >= 512 * 8 * (128 + 2) * 4
+    assert size(8, 32, 128) == 0  # one step of 32 keys
+    assert size(3, 8192, 64, splits=1 << 20) == size(3, 8192, 64, splits=8192 // 64) > 0
+    assert size(3, 8192, 64, splits=1) == 0
 
 
 def test_fastdiv_matches_division(tmp_path):

@@ -40,6 +40,42 @@ def _close(got, ref, what=""):
 
 
 @pytest.mark.parametrize("d", [32, 64, 128, 256])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("N", [1, 13, 4099, 65536])
+def test_attention_few_queries(o, d, M, N):
+    """Up to 8 queries run the VALU kernel (no padded query block): key
+    splits of whole 4096/d-key steps, a tail step past N, merged records."""
+    rng = np.random.default_rng(M * 131 + N * 7 + d)
+    q, k, v = _problem(rng, M, N, d)
+    out = _gpu.poisoned((M, d))
+    kvq.attention_online(up(q), up(k), up(v), out)
+    torch.cuda.synchronize()
+    _close(down(out), o.attention_f32(q, k, v), f"M={M} N={N} d={d}")
+
+
+@pytest.mark.parametrize("splits", [1, 2, 5, 1 << 20])
+@pytest.mark.parametrize("d", [64, 128])
+def test_attention_few_queries_peaked_and_splits(o, d, splits):
+    """Large logits (frequent rescales) in the few-query kernel under any
+    split request, and identical keys (the output is the mean of V)."""
+    rng = np.random.default_rng(d + splits)
+    M, N = 6, 3000
+    q, k, v = _problem(rng, M, N, d, qscale=8.0)
+    gq, gk, gv = up(q), up(k), up(v)
+    out = _gpu.poisoned((M, d))
+    p = kvq.attention_params(gq, gk, gv, out, num_splits=splits)
+    n = kvq.attention_workspace_size(p)
+    ws = torch.full((max(n, 1),), 0xFF, dtype=torch.uint8, device="cuda")  # NaN bytes: records need no init
+    kvq.attention(gq, gk, gv, out, num_splits=splits, workspace=ws)
+    torch.cuda.synchronize()
+    _close(down(out), o.attention_f32(q, k, v), f"peaked, splits={splits}")
+    kf = np.repeat(rng.standard_normal((1, d)).astype(np.float32), N, axis=0)
+    out = kvq.attention_online(gq, up(kf), gv)
+    torch.cuda.synchronize()
+    _close(down(out), np.broadcast_to(v.astype(np.float64).mean(0), (M, d)), "flat")
+
+
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("M,N", [(1, 1), (1, 4099), (7, 64), (128, 65), (129, 300), (200, 1000), (256, 4096),
                                  (1000, 127), (513, 2048), (63, 1024), (65, 700), (191, 256)])
 def test_attention_online_tuned(o, d, M, N):
