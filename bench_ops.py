@@ -3,7 +3,11 @@
 
   --op attention   dense fp32 attention (attention_online_launch): one head,
                    Q[M,d], K/V[N,d]; algorithmic flops 4*M*N*d (QK^T and PV)
-                   against the fp32 matrix-core peak (157.3 TFLOP/s).
+                   and bytes 4*(2*N*d + 2*M*d) (K and V read once, q read and
+                   out written).  The roofline is the fp32 matrix-core peak
+                   (157.3 TFLOP/s) when the flops per byte reach its ridge
+                   (157.3 / 8 = 19.7), else HBM (8 TB/s): decode-shaped calls
+                   (a few queries) are bandwidth-bound.
   --op prefill     prefill quantiser (kvq_prefill_quantize_launch): K and V
                    rows [B,Hkv,L,d] fp32 or bf16 into a contiguous int8 cache;
                    algorithmic bytes 2*rows*(d*in_bytes + d + 4) against HBM
@@ -96,10 +100,16 @@ def bench_attention(torch, kvq, a):
         "unit": "TFLOP/s", "us_per_call": round(us, 2), "steps": a.steps, "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"attention M{M} N{N} d{d}", "M": M, "N": N, "d": d,
                    "workspace_bytes": kvq.attention_workspace_size(p)},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
-                     "flops_per_call": flops},
     }
+    nbytes = 4.0 * (2 * N * d + 2 * M * d)
+    if flops / nbytes >= FP32_MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBPS * 1e9):
+        line["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+                            "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+                            "flops_per_call": flops}
+    else:
+        gbps = nbytes / (us * 1e-6) / 1e9
+        line["roofline"] = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                            "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes_per_call": nbytes}
     if not a.no_cpu:
         from oracle import oracle as orc  # the checker, timed as the CPU baseline
         o = orc.get()
