@@ -53,7 +53,8 @@ constexpr int kAttnMaxSplits = 1024;    // key splits per launch (the merge loop
 // ...  The weights of a query's splits, w_s = 2^(m_s - max m), come from its
 // (m, l) records (read by every column group of the query: cache hits after
 // the first); out = sum_s w_s acc_s / sum_s w_s l_s, reduced over the group
-// with shuffles.  The host picks G so that a lane sees at most 8 splits.
+// with shuffles.  The host picks G so that a lane sees at most 8 splits (up
+// to 512 splits), so the records and accumulators arrive in one round trip.
 constexpr int kMergeThreads = 256;
 template <int D>
 __global__ __launch_bounds__(kMergeThreads) void attention_merge(const AttnArgs a, int glog) {
@@ -68,11 +69,11 @@ __global__ __launch_bounds__(kMergeThreads) void attention_merge(const AttnArgs 
     const float4* acc = reinterpret_cast<const float4*>(a.part_acc) + e;
     const size_t ml_stride = static_cast<size_t>(a.M);
     const size_t acc_stride = static_cast<size_t>(a.M) * C4;
-    float mx = -INFINITY;
-    for (int sp = j; sp < S; sp += G) mx = fmaxf(mx, ml[sp * ml_stride].x);
-    for (int off = 1; off < G; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    const float ms = mx == -INFINITY ? 0.0f : mx;
-    float L = 0.0f;
+    // One pass: each chunk's records and accumulators are loaded together
+    // (one round trip per 8 splits a lane takes; one in all when the splits
+    // fit), the lane keeps a running max mr and rescales, then the group
+    // combines its lanes by their maxima.
+    float mr = -INFINITY, L = 0.0f;
     float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int s0 = j; s0 < S; s0 += 8 * G) {
         float4 x[8];
@@ -83,15 +84,36 @@ __global__ __launch_bounds__(kMergeThreads) void attention_merge(const AttnArgs 
             x[u] = acc[sp * acc_stride];
             y[u] = ml[sp * ml_stride];
         }
+        float cm = mr;
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (s0 + u * G < S) cm = fmaxf(cm, y[u].x);
+        const float c = cm == mr ? 1.0f : fast_exp2(mr - cm);
+        L *= c;
+        A.x *= c;
+        A.y *= c;
+        A.z *= c;
+        A.w *= c;
+        mr = cm;
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const float w = s0 + u * G < S ? fast_exp2(y[u].x - ms) : 0.0f;
+            const float w = s0 + u * G < S && cm != -INFINITY ? fast_exp2(y[u].x - cm) : 0.0f;
             L = fmaf(y[u].y, w, L);
             A.x = fmaf(x[u].x, w, A.x);
             A.y = fmaf(x[u].y, w, A.y);
             A.z = fmaf(x[u].z, w, A.z);
             A.w = fmaf(x[u].w, w, A.w);
         }
+    }
+    float mx = mr;
+    for (int off = 1; off < G; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    {
+        const float c = mr == -INFINITY ? 0.0f : fast_exp2(mr - mx);
+        L *= c;
+        A.x *= c;
+        A.y *= c;
+        A.z *= c;
+        A.w *= c;
     }
     for (int off = 1; off < G; off <<= 1) {
         L += __shfl_xor(L, off);
