@@ -378,6 +378,40 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     finish_split(a, unit, map, bhq0, SG, nsplit, &s_last);
 }
 
+// Log-sum-exp merge of one element over nsplit records, 8 splits' (m, l, acc)
+// loaded together per step with a running max (one round trip per 8 splits,
+// where a load-max-then-accumulate loop waits on every record in turn).
+// Every split holds at least one token, so every record's m is finite.
+__device__ inline float merge_dim_pipelined(const DecodeArgs& a, const RecMap& map, int dim, int nsplit) {
+    constexpr int kStep = 8;
+    float M = -INFINITY, L = 0.0f, A = 0.0f;
+    for (int s0 = 0; s0 < nsplit; s0 += kStep) {
+        float m[kStep], l[kStep], x[kStep];
+#pragma unroll
+        for (int u = 0; u < kStep; u++) {
+            const size_t rec = map.r0 + static_cast<size_t>(min(s0 + u, nsplit - 1)) * map.ss;
+            m[u] = get_coherent(a.part_ml + rec * 2);
+            l[u] = get_coherent(a.part_ml + rec * 2 + 1);
+            x[u] = get_coherent(a.part_acc + rec * a.d + dim);
+        }
+        float cm = M;
+#pragma unroll
+        for (int u = 0; u < kStep; u++)
+            if (s0 + u < nsplit) cm = fmaxf(cm, m[u]);
+        const float c = fast_exp2(M - cm);  // 0 on the first step (M = -inf)
+        L *= c;
+        A *= c;
+        M = cm;
+#pragma unroll
+        for (int u = 0; u < kStep; u++) {
+            const float w = s0 + u < nsplit ? fast_exp2(m[u] - cm) : 0.0f;
+            L = fmaf(l[u], w, L);
+            A = fmaf(x[u], w, A);
+        }
+    }
+    return A / L;
+}
+
 __global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a) {
     const int bhq = blockIdx.x;
     const int b = bhq / a.Hq;
@@ -386,7 +420,7 @@ __global__ __launch_bounds__(256) void merge_kernel(const DecodeArgs a) {
     if (nsplit <= 1) return;  // written directly by the decode kernel
     const RecMap map = rec_map_static(a, bhq);
     for (int dim = threadIdx.x; dim < a.d; dim += blockDim.x)
-        a.out[static_cast<size_t>(bhq) * a.d + dim] = merge_dim(a, map, 0, dim, nsplit);
+        a.out[static_cast<size_t>(bhq) * a.d + dim] = merge_dim_pipelined(a, map, dim, nsplit);
 }
 
 __global__ __launch_bounds__(kWave) void decode_generic(const DecodeArgs a) {
