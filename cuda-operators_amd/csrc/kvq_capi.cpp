@@ -387,9 +387,15 @@ AttnPlan attention_plan(int M, int N, int d, bool aligned, int requested) {
     p.tuned = kvq::attention_tuned_dim(d) && aligned;
     p.chunk = N;
     if (!p.tuned) return p;  // the generic kernel runs unsplit
-    if (const int qm = kvq::attention_rows_queries(M); qm > 0) {
-        // A few queries: the VALU kernel, one query block, key splits to
-        // fill KVQ_ATTN_ROWS_TARGET(qm) workgroups.
+    // 9-16 queries over long key ranges also run the VALU kernel, as 8-query
+    // blocks (M = 16, N = 65536: 38 us at d = 128, 23.6 at d = 64, 65.9 at
+    // d = 256, against 45.7, 28.2, 83.3 us in a padded matrix-core block); at
+    // N = 16384 (23.2 vs 16.7 us) or 24+ queries the matrix cores win.
+    int qm = kvq::attention_rows_queries(M);
+    if (qm == 0 && M <= 2 * kvq::attention_rows_queries(8) && N >= 65536) qm = kvq::attention_rows_queries(8);
+    if (qm > 0) {
+        // A few queries: the VALU kernel, query blocks of qm, key splits to
+        // fill KVQ_ATTN_ROWS_TARGET(qm) workgroups per query block.
         p.qblock = qm;
         const long long rt = kvq::attention_rows_tile(d);
         const long long rtiles = (static_cast<long long>(N) + rt - 1) / rt;

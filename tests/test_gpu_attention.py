@@ -40,11 +40,12 @@ def _close(got, ref, what=""):
 
 
 @pytest.mark.parametrize("d", [32, 64, 128, 256])
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 12, 16])
 @pytest.mark.parametrize("N", [1, 13, 4099, 65536])
 def test_attention_few_queries(o, d, M, N):
-    """Up to 8 queries run the VALU kernel (no padded query block): key
-    splits of whole 4096/d-key steps, a tail step past N, merged records."""
+    """Up to 8 queries (and 9-16 at N >= 65536, as 8-query blocks) run the
+    VALU kernel: key splits of whole 4096/d-key steps, a tail step past N,
+    merged records; 12 and 16 below 65536 keys take the matrix cores."""
     rng = np.random.default_rng(M * 131 + N * 7 + d)
     q, k, v = _problem(rng, M, N, d)
     out = _gpu.poisoned((M, d))
