@@ -332,7 +332,7 @@ __global__ __launch_bounds__(W* kWave) void attention_mfma(const AttnArgs a) {
 // attention_merge.
 constexpr int kRowsWaves = 4;
 constexpr int kRowsLoads = 4;  // float4 loads of K (and of V) in flight per lane
-constexpr int kRowsMaxQueries = 8;
+constexpr int kRowsMaxQueries = kAttnRowsBlock;
 template <int D, int QM>
 struct RowsShape {
     static constexpr int L = D == 128 && QM >= 4 ? 16 : D / 4;  // lanes per key row

@@ -392,7 +392,7 @@ AttnPlan attention_plan(int M, int N, int d, bool aligned, int requested) {
     // d = 256, against 45.7, 28.2, 83.3 us in a padded matrix-core block); at
     // N = 16384 (23.2 vs 16.7 us) or 24+ queries the matrix cores win.
     int qm = kvq::attention_rows_queries(M);
-    if (qm == 0 && M <= 2 * kvq::attention_rows_queries(8) && N >= 65536) qm = kvq::attention_rows_queries(8);
+    if (qm == 0 && M <= 2 * kvq::kAttnRowsBlock && N >= 65536) qm = kvq::kAttnRowsBlock;
     if (qm > 0) {
         // A few queries: the VALU kernel, query blocks of qm, key splits to
         // fill KVQ_ATTN_ROWS_TARGET(qm) workgroups per query block.

@@ -150,6 +150,7 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t stream);
 // workgroups (few queries, or few keys to split).
 constexpr int kAttnBlockWide = 128;
 constexpr int kAttnBlockNarrow = 64;
+constexpr int kAttnRowsBlock = 8;     // queries per workgroup of the few-query kernel, at most
 
 struct AttnArgs {
     const float* q;    // [M, d]
