@@ -283,6 +283,10 @@ def test_attention_workspace_plan(L):
     assert size(8, 32, 128) == 0  # one step of 32 keys
     assert size(3, 8192, 64, splits=1 << 20) == size(3, 8192, 64, splits=8192 // 64) > 0
     assert size(3, 8192, 64, splits=1) == 0
+    # 9-16 queries over >= 65536 keys: 8-query blocks of the same kernel, 512
+    # splits each (the matrix-core plan would take 256 splits of one block).
+    assert size(16, 65536, 128) >= 512 * 16 * (128 + 2) * 4
+    assert 0 < size(16, 16384, 128) < 512 * 16 * (128 + 2) * 4
 
 
 def test_fastdiv_matches_division(tmp_path):
