@@ -324,10 +324,11 @@ __global__ __launch_bounds__(W* kWave) void attention_mfma(const AttnArgs a) {
 // is 4096/D keys whatever L is.  Each key group keeps its own online-softmax
 // state per query; its scores are sums over the group's lanes (DPP within a
 // 16-lane row, ds_bpermute across rows).  L = D/4 (4 dims per lane), except
-// 16 at d = 128 with 4-8 queries: there the per-key cross-row sums dominated
-// the ALU time (M = 8, N = 65536: 31.7 -> 23.4 us); with fewer queries, or at
-// d = 256 (16 dims per lane, one key per lane and step), 4 dims per lane ran
-// faster.  The epilogue merges the groups of a wave (shuffles), then the waves
+// D/8 (8 dims per lane) at d >= 128 with 4-8 queries: there the per-key
+// cross-row sums dominated the ALU time (N = 65536, d = 128, M = 8: 31.7 ->
+// 23.4 us; d = 256, M = 4: 45.0 -> 29.0 us); with 1-2 queries 4 dims per lane
+// ran faster, and 16 dims per lane (one key per lane and step) slower still.
+// The epilogue merges the groups of a wave (shuffles), then the waves
 // (LDS), and writes the output, or the split's (m, l, acc) record for
 // attention_merge.
 constexpr int kRowsWaves = 4;
@@ -335,7 +336,7 @@ constexpr int kRowsLoads = 4;  // float4 loads of K (and of V) in flight per lan
 constexpr int kRowsMaxQueries = kAttnRowsBlock;
 template <int D, int QM>
 struct RowsShape {
-    static constexpr int L = D == 128 && QM >= 4 ? 16 : D / 4;  // lanes per key row
+    static constexpr int L = QM >= 4 && D >= 128 ? D / 8 : D / 4;  // lanes per key row
     static constexpr int E = D / L;                              // dims per lane
     static constexpr int NV = E / 4;                             // float4 loads per row per lane
     static constexpr int U = kRowsLoads / NV;                    // keys per lane per step
