@@ -22,11 +22,20 @@ Timing protocol:
   * cpu_baseline: the CPU oracle (same fp32 math as the reference's
     cpu_reference, OpenMP over heads) on the host copy of the same step.
 
+Besides the headline (cfg1), the same protocol runs every configuration of
+BASELINE.json (cfg0..cfg4, --configs) and reports each under "configs": us per
+step, KV GB/s, fraction of the HBM roofline, the kernel the library planned,
+the CPU baseline on a bounded sample, and max |GPU - oracle| of one checked
+step (with the fraction of the 1e-4 + 1e-3*|ref| tolerance it uses).
+"provenance" records git state, source and library hashes, ROCm/hipcc/torch
+versions, the GPU and the host CPU.
+
 Prints ONE JSON line.  Only --gpus 1 is supported (this build runs on one GPU).
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import importlib
 import json
 import math
@@ -63,6 +72,12 @@ def parse():
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="max seconds for the CPU baseline")
+    ap.add_argument("--configs", default="cfg0,cfg1,cfg2,cfg3,cfg4",
+                    help="configurations to time besides the headline, comma-separated ('none': headline only)")
+    ap.add_argument("--config-steps", type=int, default=200,
+                    help="timed steps per extra configuration (at least --steps)")
+    ap.add_argument("--config-cpu-budget", type=float, default=3.0,
+                    help="max seconds for each extra configuration's CPU baseline")
     ap.add_argument("--calib", action="store_true",
                     help="also run a plain 1 GiB copy kernel (PMC byte-counter calibration)")
     ap.add_argument("--traffic", default=os.path.join(REPO, "profiles", "traffic.json"),
@@ -70,8 +85,27 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(prob, budget_s):
-    """The oracle (fp32 reference math, OpenMP) on the host copy of one step."""
+def host_info():
+    """CPU model and the cores this process may use (the GPU box's host share)."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"cpu_model": model, "nproc": usable, "os_cpu_count": os.cpu_count()}
+
+
+def cpu_baseline(prob, budget_s, min_runs=5):
+    """The oracle (fp32 reference math, OpenMP) on the host copy of one step.
+    Returns (baseline dict, the oracle's output of that step)."""
     import numpy as np
     from oracle import oracle as orc
 
@@ -86,22 +120,96 @@ def cpu_baseline(prob, budget_s):
             o.append(kn, vn, k, v, ks, vs, positions=lengths - 1)
         return o.decode_f32(q, k, v, ks, vs, lengths=lengths)
 
-    step()  # warm-up
+    ref = step()  # warm-up; also the checked step's expected output
     times, t_start = [], time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - t_start < 2.0 and len(times) < 50):
+    while len(times) < min_runs or (time.perf_counter() - t_start < 2.0 and len(times) < 50):
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
         if time.perf_counter() - t_start > budget_s:
             break
     t = statistics.median(times)
-    return {
+    base = {
         "value": round(prob.kv_bytes() / t / 1e9, 3),
         "unit": "GB/s",
+        "us_per_step": round(t * 1e6, 1),
         "cores": o.threads,
         "kind": "port",
         "sample": (f"full {prob.name} step ({'append + ' if kn is not None else ''}decode, "
                    f"{prob.B}x{prob.Hq} query heads), median of {len(times)} runs: {t * 1e6:.0f} us/step"),
+    }
+    base.update(host_info())
+    return base, ref
+
+
+def check_step(got, ref):
+    """max |GPU - oracle| of one step and the largest fraction of the parity
+    tolerance (1e-4 + 1e-3 * |ref|) any element uses."""
+    import numpy as np
+    g = np.asarray(got, np.float64)
+    r = np.asarray(ref, np.float64)
+    err = np.abs(g - r)
+    finite = bool(np.all(np.isfinite(g)))
+    return {"max_abs_err": float(err.max()) if finite else None,
+            "max_tol_frac": float((err / (1e-4 + 1e-3 * np.abs(r))).max()) if finite else None,
+            "within_tolerance": finite and bool(np.all(err <= 1e-4 + 1e-3 * np.abs(r)))}
+
+
+def _sha256_files(paths):
+    h = hashlib.sha256()
+    for pth in sorted(paths):
+        try:
+            with open(pth, "rb") as f:
+                h.update(os.path.relpath(pth, REPO).encode())
+                h.update(f.read())
+        except OSError:
+            return None
+    return h.hexdigest()
+
+
+def provenance(torch, kvq):
+    """Where and from what this line was measured (as the reference's scan
+    harness records, benchmarks/selective_scan/run.py:91-116)."""
+    import glob
+    import subprocess
+
+    def cmd(*argv):
+        try:
+            r = subprocess.run(list(argv), capture_output=True, text=True, timeout=20)
+            return r.stdout.strip() if r.returncode == 0 else None
+        except (OSError, subprocess.SubprocessError):
+            return None
+
+    pkg = os.path.join(REPO, "cuda-operators_amd")
+    srcs = glob.glob(os.path.join(pkg, "csrc", "*")) + glob.glob(os.path.join(REPO, "include", "*.h"))
+    build_info = None
+    try:
+        with open(os.path.join(pkg, "build_info.json")) as f:
+            build_info = json.load(f)
+    except (OSError, ValueError):
+        pass
+    rocm = None
+    try:
+        with open("/opt/rocm/.info/version") as f:
+            rocm = f.read().strip()
+    except OSError:
+        pass
+    hipcc = cmd("/opt/rocm/bin/hipcc", "--version")
+    props = torch.cuda.get_device_properties(0)
+    return {
+        "git_sha": cmd("git", "-C", REPO, "rev-parse", "HEAD"),
+        "build": build_info,
+        "sources_sha256": _sha256_files(srcs),
+        "libkvq_sha256": _sha256_files([kvq.LIB_PATH]),
+        "bench_sha256": _sha256_files([os.path.abspath(__file__)]),
+        "library": kvq.version(),
+        "rocm": rocm,
+        "hipcc": hipcc.splitlines()[0] if hipcc else None,
+        "torch": torch.__version__,
+        "gpu": props.name,
+        "gpu_arch": getattr(props, "gcnArchName", None),
+        "gpu_cus": props.multi_processor_count,
+        **host_info(),
     }
 
 
@@ -132,44 +240,29 @@ def paged_decoder(kvq, p, out, page, splits, seed, order="shuffled"):
     return dec
 
 
-def kernel_name(base, page):
-    """The tuned kernel the library's planner picks for this problem."""
-    G = base.Hq // base.Hkv
-    mfma = base.d in (64, 128) and G % 4 == 0 and (page == 0 or (page & (page - 1) == 0 and page % 32 == 0))
-    name = "decode_mfma" if mfma else "decode_fast"
-    if base.uniform:
-        return name
-    # Ragged: a batch of <= 64 sequences that fits one round plans itself in
-    # the kernel (matrix-core kernel, or the FMA kernel with <= 2 query heads
-    # per kv head); otherwise a schedule_kernel launch precedes it.
-    if mfma:
-        U, slots = base.Hkv * (G // (8 if G % 8 == 0 else 4)), 256
-    else:
-        sg = 4 if G % 4 == 0 else (2 if G % 2 == 0 else 1)
-        U, slots = (base.Hkv * (G // sg) if sg <= 2 else 0), 512
-    if U and base.B <= 64 and base.B <= slots // U:
+def kernel_name(kvq, dec):
+    """The kernel (and split plan) the library planned for decoder `dec`,
+    from its host-only plan query (paged problems: the contiguous plan's
+    kernel family)."""
+    names = {kvq.KERNEL_DECODE_GENERIC: "decode_generic", kvq.KERNEL_DECODE_VALU: "decode_fast",
+             kvq.KERNEL_DECODE_MFMA: "decode_mfma"}
+    if not isinstance(dec.params, kvq.DecodeParams):
+        return "paged"
+    info = kvq.decode_plan(dec.params)
+    name = f"{names[info.kernel]}<{dec.params.head_dim},{info.heads_per_group}>"
+    if info.split_plan == kvq.SPLITS_IN_KERNEL:
         return name + " (split plan in-kernel)"
-    return name + " (+ schedule_kernel per step)"
+    if info.split_plan == kvq.SPLITS_SCHEDULE:
+        return name + " (+ schedule_kernel per step)"
+    return name + (f", {info.splits} splits" if info.splits > 1 else ", unsplit")
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              f"(sharding across GPUs is designed, not built)", file=sys.stderr)
-        sys.exit(2)
-
-    import torch
-
-    pkg = importlib.import_module("cuda-operators_amd")
-    kvq = pkg.kvq
-    synth = importlib.import_module("cuda-operators_amd.synth")
-    kvq.lib()  # fail loudly if the HIP library is missing
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
+def time_config(args, torch, kvq, synth, name, steps, settle_ms, page_size=0):
+    """Build config `name` (seeded, on the GPU), then W warm-up steps, settle,
+    K timed steps over rotated replicas, a per-launch pass and a cache-warm
+    pass.  Returns (result dict, the Problem, replica 0's output)."""
     stream = torch.cuda.current_stream()
-
-    base = synth.make(args.config, seed=args.seed, device="cuda")
+    base = synth.make(name, seed=args.seed, device="cuda")
     kv_bytes = base.kv_bytes()
     alloc_bytes = base.B * base.Hkv * base.cap * (2 * base.d + 8)
     R = args.replicas or max(3, math.ceil(512 * 2**20 / alloc_bytes))
@@ -180,8 +273,8 @@ def main():
                           base.lengths, base.k_new, base.v_new)
         reps.append(c)
     outs = [torch.empty_like(base.q) for _ in reps]
-    if args.page_size > 0:
-        decs = [paged_decoder(kvq, p, o, args.page_size, args.splits, args.seed + i, args.page_order)
+    if page_size > 0:
+        decs = [paged_decoder(kvq, p, o, page_size, args.splits, args.seed + i, args.page_order)
                 for i, (p, o) in enumerate(zip(reps, outs))]
     else:
         decs = [kvq.Decoder(p.q, p.k, p.v, p.ks, p.vs, o, lengths=p.lengths,
@@ -199,24 +292,24 @@ def main():
         decs[i % R](sh)
     torch.cuda.synchronize()
     settle = 0
-    while (time.perf_counter() - t_warm) * 1e3 < args.settle_ms:
+    while (time.perf_counter() - t_warm) * 1e3 < settle_ms:
         for _ in range(50):
             decs[(args.warmup + settle) % R](sh)
             settle += 1
         torch.cuda.synchronize()
 
-    # Pass 1: K steps between two events (the contract's timed region).
+    # Pass 1: K steps between two events on the launch stream (the timed region).
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         decs[i % R](sh)
     e1.record(stream)
     torch.cuda.synchronize()
-    ms_per_step = e0.elapsed_time(e1) / args.steps
+    ms_per_step = e0.elapsed_time(e1) / steps
 
     # Pass 2: every launch between its own events (kernel duration).
-    n2 = min(args.steps, 100)
+    n2 = min(steps, 100)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n2)]
     for i, (a, b) in enumerate(ev):
         a.record(stream)
@@ -236,6 +329,56 @@ def main():
     torch.cuda.synchronize()
     warm_ms = w0.elapsed_time(w1) / n2
 
+    gbps = kv_bytes / (ms_per_step * 1e-3) / 1e9
+    res = {
+        "workload": f"{name}: B{base.B} Hq{base.Hq} Hkv{base.Hkv} d{base.d} "
+                    f"L{'U' if not base.uniform else ''}{base.max_len}"
+                    f"{' +append' if base.k_new is not None else ''}",
+        "kernel": kernel_name(kvq, decs[0]),
+        "us_per_step": round(ms_per_step * 1e3, 3),
+        "GB/s": round(gbps, 2),
+        "frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "kv_bytes_per_step": kv_bytes,
+        "steps": steps,
+        "settle_steps": settle,
+        "replicas": R,
+        "kernel_us_isolated": round(kern_ms * 1e3, 3),
+        "cache_warm_us_per_step": round(warm_ms * 1e3, 3),
+        "splits": decs[0].params.num_splits or "auto",
+    }
+    out0 = outs[0]
+    del decs, reps
+    return res, base, out0
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(sharding across GPUs is designed, not built)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    pkg = importlib.import_module("cuda-operators_amd")
+    kvq = pkg.kvq
+    synth = importlib.import_module("cuda-operators_amd.synth")
+    kvq.lib()  # fail loudly if the HIP library is missing
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    head, base, out0 = time_config(args, torch, kvq, synth, args.config, args.steps, args.settle_ms,
+                                   args.page_size)
+    kv_bytes = head["kv_bytes_per_step"]
+    ms_per_step = head["us_per_step"] * 1e-3
+    head_check = None
+    head_cpu = None
+    if not args.no_cpu:
+        head_cpu, ref = cpu_baseline(base, args.cpu_budget)
+        head_check = check_step(out0.cpu().numpy(), ref)
+    del base, out0
+    torch.cuda.empty_cache()
+
     if args.calib:
         x = torch.empty(2**28, dtype=torch.float32, device=dev)  # 1 GiB
         y = torch.empty_like(x)
@@ -248,11 +391,12 @@ def main():
     gbps = kv_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = gbps  # the step's decode launch(es)
     traffic = None
+    traffic_all = {}
     if os.path.exists(args.traffic):
         try:
             with open(args.traffic) as f:
-                tr = json.load(f)
-            entry = tr.get("configs", {}).get(args.config)
+                traffic_all = json.load(f).get("configs", {})
+            entry = traffic_all.get(args.config)
             # Measured for the contiguous cache with the library's split choice.
             if entry and args.page_size == 0 and args.splits == 0:
                 traffic = entry.get("hbm_bytes_per_launch")
@@ -266,7 +410,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "settle_steps": settle,
+        "settle_steps": head["settle_steps"],
         "ms_per_step": round(ms_per_step, 6),
         "us_per_step": round(ms_per_step * 1e3, 3),
         "pct_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
@@ -277,34 +421,58 @@ def main():
         "storage": "int8 K/V + fp32 per-token scales",
         "data": "synthetic (seeded N(0,1) fp32 quantised per token on device)",
         "config": {
-            "workload": f"{args.config}: B{base.B} Hq{base.Hq} Hkv{base.Hkv} d{base.d} "
-                        f"L{'U' if not base.uniform else ''}{base.max_len}"
-                        f"{' +append' if base.k_new is not None else ''}",
+            "workload": head["workload"],
             "kv_bytes_per_step": kv_bytes,
-            "replicas": R,
-            "splits": decs[0].params.num_splits or "auto",
+            "replicas": head["replicas"],
+            "splits": head["splits"],
             "layout": (f"paged, {args.page_size} tokens per page, {args.page_order} pool" if args.page_size > 0
                        else "contiguous"),
             "parallelism": "single GPU",
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": kernel_name(base, args.page_size),
+            "kernel": head["kernel"],
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "kernel_us": round(ms_per_step * 1e3, 3),
-            "kernel_us_isolated": round(kern_ms * 1e3, 3),
+            "kernel_us_isolated": head["kernel_us_isolated"],
             "bytes_per_launch": kv_bytes,
         },
-        "cache_warm": {"us_per_step": round(warm_ms * 1e3, 3),
-                       "GB/s": round(kv_bytes / (warm_ms * 1e-3) / 1e9, 2),
+        "cache_warm": {"us_per_step": head["cache_warm_us_per_step"],
+                       "GB/s": round(kv_bytes / (head["cache_warm_us_per_step"] * 1e-6) / 1e9, 2),
                        "note": "single replica, Infinity-Cache resident; not the headline"},
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(base, args.cpu_budget)
+    if head_cpu is not None:
+        line["cpu_baseline"] = head_cpu
+        line["parity"] = head_check
+
+    # Every other configuration under the same protocol.
+    wanted = [] if args.configs.strip() in ("", "none") else [c.strip() for c in args.configs.split(",")]
+    configs = {}
+    for name in wanted:
+        if name == args.config and args.page_size == 0:
+            res = {k: head[k] for k in ("workload", "kernel", "us_per_step", "GB/s", "frac", "kv_bytes_per_step",
+                                        "steps", "replicas", "kernel_us_isolated", "cache_warm_us_per_step")}
+            if head_cpu is not None:
+                res["cpu_baseline"] = head_cpu
+                res.update(head_check)
+        else:
+            res, base, out0 = time_config(args, torch, kvq, synth, name, max(args.steps, args.config_steps),
+                                          min(args.settle_ms, 200.0))
+            if not args.no_cpu:
+                res["cpu_baseline"], ref = cpu_baseline(base, args.config_cpu_budget, min_runs=3)
+                res.update(check_step(out0.cpu().numpy(), ref))
+            del base, out0
+            torch.cuda.empty_cache()
+        tr = traffic_all.get(name)
+        res["traffic"] = tr.get("hbm_bytes_per_launch") if tr else None
+        configs[name] = res
+    if configs:
+        line["configs"] = configs
+    line["provenance"] = provenance(torch, kvq)
     print(json.dumps(line), flush=True)
 
 

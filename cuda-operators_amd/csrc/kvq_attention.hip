@@ -624,7 +624,7 @@ void launch_mfma_attention_d(const AttnArgs& a, int glog, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
-    if (attention_tuned_dim(a.d)) {
+    if (a.tuned && attention_tuned_dim(a.d)) {
         int glog = 0;  // lanes per merge group: at most 8 splits per lane, at most a wave
         while (glog < 6 && ((a.splits - 1) >> glog) >= 8) glog++;
         switch (a.d) {

@@ -7,11 +7,13 @@
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include <algorithm>
 #include <functional>
 #include <map>
 #include <mutex>
+#include <vector>
 
 #include "../../include/kvq.h"
 #include "kvq_internal.hpp"
@@ -74,6 +76,53 @@ constexpr long kMinSplitUnitBytes = 192 * 1024;
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Diagnostic switches, read once from the environment on first use:
+// * KVQ_DEBUG_SYNC: on ("1", "true", "yes", "on"), every launching entry point
+//   synchronises its stream after its launches and returns the first error,
+//   so an asynchronous fault is reported by the call that caused it (the
+//   reference's compile-time KV_CUDA_DEBUG_SYNC,
+//   kv_cache/KV_int8_split_optimized.cu:16-18,253-264).  Skipped while the
+//   stream is being captured into a graph.
+// * KVQ_FORCE_KERNEL: "valu" keeps decode plans off the matrix-core kernel,
+//   "generic" off both tuned kernels, so one problem can be profiled on either
+//   kernel.  Any other value changes nothing.
+bool env_on(const char* name) {
+    const char* s = getenv(name);
+    if (!s) return false;
+    static const char* const kOn[] = {"1", "true", "yes", "on", "TRUE", "YES", "ON", "True", "Yes", "On"};
+    for (const char* o : kOn)
+        if (strcmp(s, o) == 0) return true;
+    return false;
+}
+
+bool debug_sync() {
+    static const bool on = env_on("KVQ_DEBUG_SYNC");
+    return on;
+}
+
+enum ForcedKernel { kForceNone = 0, kForceValu = 1, kForceGeneric = 2 };
+
+int forced_kernel() {
+    static const int k = [] {
+        const char* s = getenv("KVQ_FORCE_KERNEL");
+        if (s && strcmp(s, "valu") == 0) return static_cast<int>(kForceValu);
+        if (s && strcmp(s, "generic") == 0) return static_cast<int>(kForceGeneric);
+        return static_cast<int>(kForceNone);
+    }();
+    return k;
+}
+
+// Every launching entry point returns through here.
+hipError_t finish_call(hipError_t err, hipStream_t stream) {
+    if (err != hipSuccess || !debug_sync()) return err;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    err = hipStreamIsCapturing(stream, &st);
+    if (err != hipSuccess || st != hipStreamCaptureStatusNone) return err;
+    err = hipStreamSynchronize(stream);
+    if (err != hipSuccess) return err;
+    return hipGetLastError();
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Split count and workspace layout for one decode problem.
@@ -96,6 +145,9 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
     const bool valu_pages = page == 0 || (pow2 && wave_tokens > 0 && page % wave_tokens == 0);
     const bool mfma_pages = page == 0 || (pow2 && page % 32 == 0 && page < (1 << 24));
     int tile = 0;
+    const int force = forced_kernel();
+    if (force == kForceGeneric) aligned = false;
+    if (force == kForceValu) quads = false;
     if (aligned && quads && mfma_pages && sg_m > 0) {
         p.kernel = kvq::Kernel::Mfma;
         p.sg = sg_m;
@@ -230,8 +282,25 @@ DecodeArgs reference_args(const float* Q, const int8_t* K, const int8_t* V, cons
     return a;
 }
 
-bool reference_aligned(const float* Q, const int8_t* K, const int8_t* V, int d) {
+bool reference_aligned(const void* Q, const void* K, const void* V, int d) {
     return aligned16(Q) && aligned16(K) && aligned16(V) && (d % 16) == 0;
+}
+
+// Plan of kv_int8_split_launch / kv_int8_simple_launch, whose workspace is the
+// caller's S of H*N floats.  A split needs (d + 2) floats of records per head,
+// but the (m, l) region is padded to kAlign bytes before the accumulators, so
+// N / (d + 2) splits can still overrun S by up to kAlign bytes at small H
+// (H = 1, N = 516, d = 256: 2 splits need 2304 bytes of a 2064-byte S).  The
+// split count therefore steps down until the whole layout fits.
+DecodePlan reference_plan(int H, int N, int d, bool aligned) {
+    const size_t cap = static_cast<size_t>(H) * static_cast<size_t>(N) * sizeof(float);
+    int max_splits = std::max(1, N / (d + 2));
+    DecodePlan p = make_plan(1, H, H, d, N, aligned, false, 0, false, 0, max_splits, false);
+    while (p.splits > 1 && plan_bytes(p) > cap) {
+        max_splits = p.splits - 1;
+        p = make_plan(1, H, H, d, N, aligned, false, 0, false, 0, max_splits, false);
+    }
+    return p;
 }
 
 hipError_t reference_launch(const float* Q, const int8_t* K, const int8_t* V, const float* ks,
@@ -240,14 +309,12 @@ hipError_t reference_launch(const float* Q, const int8_t* K, const int8_t* V, co
     if (!Q || !K || !V || !ks || !vs || !out || !S || !shape_ok(H, N, d)) return hipErrorInvalidValue;
     if (static_cast<long long>(H) * N > INT_MAX) return hipErrorInvalidValue;
     DecodeArgs a = reference_args(Q, K, V, ks, vs, out, H, N, d);
-    // S holds H*N floats; a split needs (d + 2) floats per head.
-    const int max_splits = std::max(1, N / (d + 2));
-    const DecodePlan p = make_plan(1, H, H, d, N, reference_aligned(Q, K, V, d), false, 0, false, 0, max_splits, false);
+    const DecodePlan p = reference_plan(H, N, d, reference_aligned(Q, K, V, d));
     a.splits = p.splits;
     a.chunk = p.chunk;
     a.nsg = p.nsg;
     bind_workspace(a, p, S);
-    return kvq::launch_decode(a, p, stream);
+    return finish_call(kvq::launch_decode(a, p, stream), stream);
 }
 
 // Library-owned, per-device split workspace for the legacy `solve` ABI.  Grown
@@ -288,6 +355,20 @@ hipError_t with_solve_workspace(size_t need, Launch&& launch) {
     return launch(w.ptr);
 }
 
+kvq_plan_info decode_info(const DecodePlan& p) {
+    kvq_plan_info r{};
+    r.kernel = p.kernel == kvq::Kernel::Mfma   ? KVQ_KERNEL_DECODE_MFMA
+               : p.kernel == kvq::Kernel::Valu ? KVQ_KERNEL_DECODE_VALU
+                                               : KVQ_KERNEL_DECODE_GENERIC;
+    r.heads_per_group = p.sg;
+    r.split_plan = p.fit ? KVQ_SPLITS_IN_KERNEL : p.scheduled ? KVQ_SPLITS_SCHEDULE : KVQ_SPLITS_STATIC;
+    r.splits = r.split_plan == KVQ_SPLITS_STATIC ? p.splits : 0;
+    r.chunk = r.split_plan == KVQ_SPLITS_STATIC ? p.chunk : 0;
+    r.query_block = 0;
+    r.workspace_bytes = plan_bytes(p);
+    return r;
+}
+
 bool decode_params_ok(const kvq_decode_params* p) {
     if (!p) return false;
     if (p->batch <= 0 || p->num_q_heads <= 0 || p->num_kv_heads <= 0) return false;
@@ -304,6 +385,37 @@ bool decode_params_ok(const kvq_decode_params* p) {
 }
 
 int decode_max_len(const kvq_decode_params* p) { return p->max_seq_len > 0 ? p->max_seq_len : p->capacity; }
+
+// Launches a validated decode problem under `plan` with a workspace of at
+// least plan_bytes(plan) (zero-filled counter prefix).
+hipError_t decode_run(const kvq_decode_params* p, const DecodePlan& plan, void* workspace, hipStream_t stream) {
+    DecodeArgs a{};
+    a.q = p->q;
+    a.k = p->k_cache;
+    a.v = p->v_cache;
+    a.ks = p->k_scale;
+    a.vs = p->v_scale;
+    a.out = p->out;
+    a.lengths = p->lengths;
+    a.k_new = p->k_new;
+    a.v_new = p->v_new;
+    a.B = p->batch;
+    a.Hq = p->num_q_heads;
+    a.Hkv = p->num_kv_heads;
+    a.G = p->num_q_heads / p->num_kv_heads;
+    a.cap = p->capacity;
+    a.d = p->head_dim;
+    a.uniform_len = decode_max_len(p);
+    a.max_len = decode_max_len(p);
+    a.splits = plan.splits;
+    a.chunk = plan.chunk;
+    a.nsg = plan.nsg;
+    const float scale = p->softmax_scale > 0.0f ? p->softmax_scale : 1.0f / sqrtf(static_cast<float>(p->head_dim));
+    a.scale_log2 = scale * kLog2e;
+    bind_workspace(a, plan, workspace);
+    return kvq::launch_decode(a, plan, stream);
+}
+
 
 bool decode_aligned(const kvq_decode_params* p) {
     return aligned16(p->q) && aligned16(p->k_cache) && aligned16(p->v_cache) && (p->head_dim % 16) == 0 &&
@@ -456,6 +568,7 @@ hipError_t attention_run(int M, int N, int d, const float* q, const float* k, co
     a.splits = p.splits;
     a.chunk = p.chunk;
     a.qblock = p.qblock;
+    a.tuned = p.tuned;
     a.scale_log2 = scale * 1.4426950408889634f;
     if (p.splits > 1) {
         char* base = static_cast<char*>(ws);
@@ -466,11 +579,14 @@ hipError_t attention_run(int M, int N, int d, const float* q, const float* k, co
 }
 
 // Library-owned attention workspaces, one per (device, stream): launches on
-// one stream are ordered and may share one; different streams must not.
-// Grown on demand (hipFree waits for in-flight work); the split records need
-// no initial contents.  As for `solve`, `launch(ptr)` is enqueued under the
-// lock, so a concurrent call on the same stream cannot free the workspace
-// before this launch exists.
+// one stream are ordered and may share one; different streams must not.  The
+// split records need no initial contents.  Grown on demand to at least twice
+// the old size; a superseded workspace is never freed, because a graph
+// captured from an earlier call on this stream still writes to it on every
+// replay (so the retired bytes stay below the live ones).  Growing needs
+// hipMalloc, which a capturing stream does not allow: run one eager call of
+// the largest problem before capturing.  As for `solve`, `launch(ptr)` is
+// enqueued under the lock.
 struct AttnWorkspaceKey {
     int device;
     hipStream_t stream;
@@ -480,6 +596,7 @@ struct AttnWorkspaceKey {
 };
 std::mutex g_attn_ws_mutex;
 std::map<AttnWorkspaceKey, SolveWorkspace> g_attn_ws;
+std::vector<void*> g_attn_retired;
 
 template <class Launch>
 hipError_t with_attention_workspace(size_t need, hipStream_t stream, Launch&& launch) {
@@ -490,15 +607,12 @@ hipError_t with_attention_workspace(size_t need, hipStream_t stream, Launch&& la
     std::lock_guard<std::mutex> lock(g_attn_ws_mutex);
     SolveWorkspace& w = g_attn_ws[AttnWorkspaceKey{dev, stream}];
     if (w.bytes < need) {
-        if (w.ptr) {
-            err = hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.bytes = 0;
-            if (err != hipSuccess) return err;
-        }
-        const size_t bytes = round_up(need, 1 << 20);
-        err = hipMalloc(&w.ptr, bytes);
+        const size_t bytes = round_up(std::max(need, 2 * w.bytes), 1 << 20);
+        void* ptr = nullptr;
+        err = hipMalloc(&ptr, bytes);
         if (err != hipSuccess) return err;
+        if (w.ptr) g_attn_retired.push_back(w.ptr);  // still referenced by any graph captured before
+        w.ptr = ptr;
         w.bytes = bytes;
     }
     return launch(w.ptr);
@@ -527,10 +641,10 @@ void solve(const float* Q, const int8_t* K_int8, const int8_t* V_int8, const flo
     a.splits = p.splits;
     a.chunk = p.chunk;
     a.nsg = p.nsg;
-    const hipError_t err = with_solve_workspace(plan_bytes(p), [&](void* ws) {
+    const hipError_t err = finish_call(with_solve_workspace(plan_bytes(p), [&](void* ws) {
         bind_workspace(a, p, ws);
         return kvq::launch_decode(a, p, nullptr);
-    });
+    }), nullptr);
     if (err != hipSuccess) fprintf(stderr, "[kvq] solve: HIP error: %s (%s)\n", hipGetErrorName(err), hipGetErrorString(err));
 }
 
@@ -554,7 +668,7 @@ size_t kvq_decode_workspace_size(const kvq_decode_params* p) {
 hipError_t kvq_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (workspace_bytes == 0) return hipSuccess;
     if (!workspace) return hipErrorInvalidValue;
-    return kvq::launch_fill_zero(workspace, workspace_bytes, stream);
+    return finish_call(kvq::launch_fill_zero(workspace, workspace_bytes, stream), stream);
 }
 
 hipError_t kvq_decode_launch(const kvq_decode_params* p, void* workspace, size_t workspace_bytes,
@@ -563,31 +677,7 @@ hipError_t kvq_decode_launch(const kvq_decode_params* p, void* workspace, size_t
     const DecodePlan plan = decode_plan(p);
     const size_t need = plan_bytes(plan);
     if (need > 0 && (!workspace || workspace_bytes < need)) return hipErrorInvalidValue;
-    DecodeArgs a{};
-    a.q = p->q;
-    a.k = p->k_cache;
-    a.v = p->v_cache;
-    a.ks = p->k_scale;
-    a.vs = p->v_scale;
-    a.out = p->out;
-    a.lengths = p->lengths;
-    a.k_new = p->k_new;
-    a.v_new = p->v_new;
-    a.B = p->batch;
-    a.Hq = p->num_q_heads;
-    a.Hkv = p->num_kv_heads;
-    a.G = p->num_q_heads / p->num_kv_heads;
-    a.cap = p->capacity;
-    a.d = p->head_dim;
-    a.uniform_len = decode_max_len(p);
-    a.max_len = decode_max_len(p);
-    a.splits = plan.splits;
-    a.chunk = plan.chunk;
-    a.nsg = plan.nsg;
-    const float scale = p->softmax_scale > 0.0f ? p->softmax_scale : 1.0f / sqrtf(static_cast<float>(p->head_dim));
-    a.scale_log2 = scale * kLog2e;
-    bind_workspace(a, plan, workspace);
-    return kvq::launch_decode(a, plan, stream);
+    return finish_call(decode_run(p, plan, workspace, stream), stream);
 }
 
 hipError_t kvq_append_launch(const kvq_append_params* p, hipStream_t stream) {
@@ -595,9 +685,11 @@ hipError_t kvq_append_launch(const kvq_append_params* p, hipStream_t stream) {
         p->capacity <= 0 || !p->k_new || !p->v_new || !p->k_cache || !p->v_cache || !p->k_scale || !p->v_scale)
         return hipErrorInvalidValue;
     if (static_cast<long long>(p->batch) * p->num_kv_heads > INT_MAX) return hipErrorInvalidValue;
-    return kvq::launch_append(p->k_new, p->v_new, p->k_cache, p->v_cache, p->k_scale, p->v_scale, p->positions,
-                              p->uniform_position, false, p->batch, p->num_kv_heads, p->capacity,
-                              p->capacity, p->head_dim, kvq::PageMap{nullptr, 0, 0, 0, -1}, stream);
+    return finish_call(kvq::launch_append(p->k_new, p->v_new, p->k_cache, p->v_cache, p->k_scale, p->v_scale,
+                                          p->positions, p->uniform_position, false, p->batch, p->num_kv_heads,
+                                          p->capacity, p->capacity, p->head_dim,
+                                          kvq::PageMap{nullptr, 0, 0, 0, -1}, stream),
+                       stream);
 }
 
 hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, int8_t* q, float* scale,
@@ -619,9 +711,9 @@ hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, 
         a.rows = static_cast<unsigned>(rows);
         a.planes = 1;
         a.pages = kvq::PageMap{nullptr, 0, 0, 0, -1};
-        return kvq::launch_prefill(a, head_dim, false, true, stream);
+        return finish_call(kvq::launch_prefill(a, head_dim, false, true, stream), stream);
     }
-    return kvq::launch_quantize_rows(x, rows, head_dim, q, scale, stream);
+    return finish_call(kvq::launch_quantize_rows(x, rows, head_dim, q, scale, stream), stream);
 }
 
 size_t kvq_paged_decode_workspace_size(const kvq_paged_decode_params* p) {
@@ -660,7 +752,7 @@ hipError_t kvq_paged_decode_launch(const kvq_paged_decode_params* p, void* works
     const float scale = p->softmax_scale > 0.0f ? p->softmax_scale : 1.0f / sqrtf(static_cast<float>(p->head_dim));
     a.scale_log2 = scale * kLog2e;
     bind_workspace(a, plan, workspace);
-    return kvq::launch_decode(a, plan, stream);
+    return finish_call(kvq::launch_decode(a, plan, stream), stream);
 }
 
 hipError_t kvq_paged_append_launch(const kvq_paged_append_params* p, hipStream_t stream) {
@@ -672,10 +764,12 @@ hipError_t kvq_paged_append_launch(const kvq_paged_append_params* p, hipStream_t
     if (cap > INT_MAX || static_cast<long long>(p->batch) * p->num_kv_heads > INT_MAX ||
         static_cast<long long>(p->batch) * p->max_pages_per_seq > INT_MAX)
         return hipErrorInvalidValue;
-    return kvq::launch_append(p->k_new, p->v_new, p->k_pages, p->v_pages, p->k_scale_pages, p->v_scale_pages,
-                              p->positions, p->uniform_position, false, p->batch, p->num_kv_heads,
-                              static_cast<int>(cap), static_cast<int>(cap), p->head_dim,
-                              page_map(p->block_table, p->page_size, p->max_pages_per_seq, p->num_pages), stream);
+    return finish_call(
+        kvq::launch_append(p->k_new, p->v_new, p->k_pages, p->v_pages, p->k_scale_pages, p->v_scale_pages,
+                           p->positions, p->uniform_position, false, p->batch, p->num_kv_heads,
+                           static_cast<int>(cap), static_cast<int>(cap), p->head_dim,
+                           page_map(p->block_table, p->page_size, p->max_pages_per_seq, p->num_pages), stream),
+        stream);
 }
 
 hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t stream) {
@@ -715,16 +809,16 @@ hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t 
     a.planes = 2;
     const bool vec_ok = aligned16(p->k_new) && aligned16(p->v_new) &&
                         ((reinterpret_cast<uintptr_t>(p->k_cache) | reinterpret_cast<uintptr_t>(p->v_cache)) & 7u) == 0;
-    return kvq::launch_prefill(a, p->head_dim, p->dtype == KVQ_DTYPE_BF16, vec_ok, stream);
+    return finish_call(kvq::launch_prefill(a, p->head_dim, p->dtype == KVQ_DTYPE_BF16, vec_ok, stream), stream);
 }
 
 hipError_t attention_online_launch(const float* Q, const float* K, const float* V, float* output, int M, int N,
                                    int d, hipStream_t stream) {
     if (!attention_args_ok(M, N, d, Q, K, V, output)) return hipErrorInvalidValue;
     const AttnPlan p = attention_plan(M, N, d, attention_aligned(Q, K, V, output), 0);
-    return with_attention_workspace(p.bytes(), stream, [&](void* ws) {
+    return finish_call(with_attention_workspace(p.bytes(), stream, [&](void* ws) {
         return attention_run(M, N, d, Q, K, V, output, 1.0f / sqrtf(static_cast<float>(d)), p, ws, stream);
-    });
+    }), stream);
 }
 
 size_t kvq_attention_workspace_size(const kvq_attention_params* p) {
@@ -741,9 +835,45 @@ hipError_t kvq_attention_launch(const kvq_attention_params* p, void* workspace, 
     if (plan.bytes() > 0 && (!workspace || workspace_bytes < plan.bytes() || !aligned16(workspace)))
         return hipErrorInvalidValue;
     const float scale = p->softmax_scale != 0.0f ? p->softmax_scale : 1.0f / sqrtf(static_cast<float>(p->d));
-    return attention_run(p->M, p->N, p->d, p->q, p->k, p->v, p->out, scale, plan, workspace, stream);
+    return finish_call(attention_run(p->M, p->N, p->d, p->q, p->k, p->v, p->out, scale, plan, workspace, stream),
+                       stream);
 }
 
-const char* kvq_version(void) { return "kvq 0.1.0 gfx950"; }
+const char* kvq_version(void) { return "kvq 0.2.0 gfx950"; }
+
+hipError_t kvq_reference_plan(const float* Q, const int8_t* K_int8, const int8_t* V_int8, int num_heads,
+                              int seq_len, int head_dim, kvq_plan_info* info) {
+    if (!info || !Q || !K_int8 || !V_int8 || !shape_ok(num_heads, seq_len, head_dim) ||
+        static_cast<long long>(num_heads) * seq_len > INT_MAX)
+        return hipErrorInvalidValue;
+    *info = decode_info(reference_plan(num_heads, seq_len, head_dim, reference_aligned(Q, K_int8, V_int8, head_dim)));
+    return hipSuccess;
+}
+
+hipError_t kvq_decode_plan(const kvq_decode_params* p, kvq_plan_info* info) {
+    if (!info || !decode_params_ok(p)) return hipErrorInvalidValue;
+    *info = decode_info(decode_plan(p));
+    return hipSuccess;
+}
+
+hipError_t kvq_attention_plan(const kvq_attention_params* p, kvq_plan_info* info) {
+    if (!info || !p || !attention_args_ok(p->M, p->N, p->d, p->q, p->k, p->v, p->out) || p->num_splits < 0)
+        return hipErrorInvalidValue;
+    const AttnPlan plan = attention_plan(p->M, p->N, p->d, attention_aligned(p->q, p->k, p->v, p->out), p->num_splits);
+    kvq_plan_info r{};
+    if (!plan.tuned) r.kernel = KVQ_KERNEL_ATTENTION_GENERIC;
+    else if (plan.qblock <= kvq::kAttnRowsBlock) r.kernel = KVQ_KERNEL_ATTENTION_ROWS;
+    else r.kernel = KVQ_KERNEL_ATTENTION_MFMA;
+    r.heads_per_group = 1;
+    r.splits = plan.splits;
+    r.chunk = plan.chunk;
+    r.split_plan = KVQ_SPLITS_STATIC;
+    r.query_block = plan.tuned ? plan.qblock : 0;
+    r.workspace_bytes = plan.bytes();
+    *info = r;
+    return hipSuccess;
+}
+
+int kvq_diagnostics(void) { return (debug_sync() ? 1 : 0) | (forced_kernel() << 4); }
 
 }  // extern "C"

@@ -164,6 +164,8 @@ struct AttnArgs {
     int qblock;         // queries per workgroup: kAttnBlockWide or kAttnBlockNarrow (matrix cores),
                         // or 1, 2, 4, 8 (few-query kernel, attention_rows)
     float scale_log2;   // softmax scale * log2(e)
+    bool tuned;         // a tuned kernel runs (tuned head dim and 16-byte aligned q, k, v, out);
+                        // otherwise attention_generic, unsplit
 };
 int attention_tuned_dim(int d);   // the matrix-core kernel handles head dim d
 int attention_key_tile(int d);    // keys per LDS tile of the matrix-core kernel at head dim d

@@ -21,6 +21,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkvq.so")
+ATTN_LIB_PATH = os.path.join(HERE, "libkvq_attention.so")
 
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
@@ -28,6 +29,7 @@ MAX_HEAD_DIM = 4096
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
+_attn_lib: ctypes.CDLL | None = None
 
 _vp = ctypes.c_void_p
 _int = ctypes.c_int
@@ -99,11 +101,24 @@ class AttentionParams(ctypes.Structure):
         ("softmax_scale", ctypes.c_float), ("num_splits", _int),
     ]
 
+class PlanInfo(ctypes.Structure):
+    """struct kvq_plan_info (include/kvq.h part 6)."""
+    _fields_ = [
+        ("kernel", _int), ("heads_per_group", _int), ("splits", _int), ("chunk", _int),
+        ("split_plan", _int), ("query_block", _int), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+KERNEL_DECODE_GENERIC, KERNEL_DECODE_VALU, KERNEL_DECODE_MFMA = 0, 1, 2
+KERNEL_ATTENTION_MFMA, KERNEL_ATTENTION_ROWS, KERNEL_ATTENTION_GENERIC = 3, 4, 5
+SPLITS_STATIC, SPLITS_IN_KERNEL, SPLITS_SCHEDULE = 0, 1, 2
+
 EXPORTS = ("solve", "kv_int8_split_launch", "kv_int8_simple_launch", "kvq_decode_workspace_size",
            "kvq_workspace_init", "kvq_decode_launch", "kvq_append_launch", "kvq_quantize_rows_launch",
            "kvq_paged_decode_workspace_size", "kvq_paged_decode_launch", "kvq_paged_append_launch",
            "kvq_prefill_quantize_launch", "attention_online_launch", "kvq_attention_workspace_size",
-           "kvq_attention_launch", "kvq_version")
+           "kvq_attention_launch", "kvq_version", "kvq_reference_plan", "kvq_decode_plan", "kvq_attention_plan",
+           "kvq_diagnostics")
 
 
 class KvqError(RuntimeError):
@@ -152,8 +167,33 @@ def lib() -> ctypes.CDLL:
         L.kvq_attention_launch.argtypes = [ctypes.POINTER(AttentionParams), _vp, ctypes.c_size_t, _vp]
         L.kvq_attention_launch.restype = _int
         L.kvq_version.restype = ctypes.c_char_p
+        L.kvq_reference_plan.argtypes = [_vp, _vp, _vp, _int, _int, _int, ctypes.POINTER(PlanInfo)]
+        L.kvq_reference_plan.restype = _int
+        L.kvq_decode_plan.argtypes = [ctypes.POINTER(DecodeParams), ctypes.POINTER(PlanInfo)]
+        L.kvq_decode_plan.restype = _int
+        L.kvq_attention_plan.argtypes = [ctypes.POINTER(AttentionParams), ctypes.POINTER(PlanInfo)]
+        L.kvq_attention_plan.restype = _int
+        L.kvq_diagnostics.restype = _int
         _lib = L
         return L
+
+
+def attention_lib() -> ctypes.CDLL:
+    """Load libkvq_attention.so (include/kvq_attention.h): the dense-attention
+    `solve` of attention/softmax_new.cu:283-287, whose symbol libkvq.so's
+    decode `solve` already takes."""
+    global _attn_lib
+    lib()
+    with _lock:
+        if _attn_lib is not None:
+            return _attn_lib
+        if not os.path.exists(ATTN_LIB_PATH):
+            raise RuntimeError(f"libkvq_attention.so is not built ({ATTN_LIB_PATH}); run __graft_entry__.build()")
+        A = ctypes.CDLL(ATTN_LIB_PATH)
+        A.solve.argtypes = [_vp] * 4 + [_int] * 3
+        A.solve.restype = None
+        _attn_lib = A
+        return A
 
 
 def version() -> str:
@@ -416,6 +456,15 @@ def attention_online(q, k, v, out=None, stream=None) -> torch.Tensor:
     return out
 
 
+def attention_solve(q, k, v, out=None) -> torch.Tensor:
+    """The reference's compatibility `solve(Q, K, V, output, M, N, d)` of
+    attention/softmax_new.cu:283-287 (libkvq_attention.so): asynchronous on the
+    null stream, errors not reported."""
+    M, N, d, out = _attention_shapes(q, k, v, out)
+    attention_lib().solve(_ptr(q), _ptr(k), _ptr(v), _ptr(out), M, N, d)
+    return out
+
+
 def attention_params(q, k, v, out, softmax_scale: float = 0.0, num_splits: int = 0) -> AttentionParams:
     M, N, d, out = _attention_shapes(q, k, v, out)
     return AttentionParams(M, N, d, _ptr(q), _ptr(k), _ptr(v), _ptr(out), float(softmax_scale), int(num_splits))
@@ -441,6 +490,33 @@ def attention(q, k, v, out=None, softmax_scale: float = 0.0, num_splits: int = 0
     return out
 
 
+def reference_plan(H: int, N: int, d: int, q_ptr: int = 256, k_ptr: int = 4096, v_ptr: int = 8192) -> PlanInfo:
+    """Plan of kv_int8_split_launch for [H, N, d] (host-only; the pointers only
+    set the alignment)."""
+    info = PlanInfo()
+    _check("kvq_reference_plan", lib().kvq_reference_plan(q_ptr, k_ptr, v_ptr, H, N, d, ctypes.byref(info)))
+    return info
+
+
+def decode_plan(p: DecodeParams) -> PlanInfo:
+    """Plan of kvq_decode_launch for p (host-only)."""
+    info = PlanInfo()
+    _check("kvq_decode_plan", lib().kvq_decode_plan(ctypes.byref(p), ctypes.byref(info)))
+    return info
+
+
+def attention_plan(p: AttentionParams) -> PlanInfo:
+    """Plan of kvq_attention_launch for p (host-only)."""
+    info = PlanInfo()
+    _check("kvq_attention_plan", lib().kvq_attention_plan(ctypes.byref(p), ctypes.byref(info)))
+    return info
+
+
+def diagnostics() -> int:
+    """kvq_diagnostics(): bit 0 KVQ_DEBUG_SYNC, bits 4-7 KVQ_FORCE_KERNEL."""
+    return int(lib().kvq_diagnostics())
+
+
 def default_softmax_scale(d: int) -> float:
     """1/sqrtf(d) in fp32, as kv_cache/KV_int8_split_optimized.cu:335."""
     import numpy as np
@@ -458,4 +534,5 @@ __all__ = ["lib", "version", "solve", "kv_int8_split_launch", "DecodeParams", "A
            "append", "quantize_rows", "kv_bytes", "KvqError", "EXPORTS", "PagedDecodeParams",
            "PagedAppendParams", "PagedDecoder", "paged_append", "PrefillParams", "prefill", "DTYPE_F32",
            "DTYPE_BF16", "AttentionParams", "attention_online", "attention_params", "attention_workspace_size",
-           "attention"]
+           "attention", "PlanInfo", "reference_plan", "decode_plan", "attention_plan", "diagnostics",
+           "attention_lib", "attention_solve"]

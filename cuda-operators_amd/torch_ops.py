@@ -24,9 +24,11 @@ allocates nothing once its workspace exists.
 
 Workspaces are cached per (operator, device, stream) and grown on demand:
 launches on one stream are ordered, so they may share one; launches on
-different streams get different ones.  A graph capture should be preceded by
-one eager call of the same problem, so that the workspace (allocated, and
-zero-filled by a kernel, never a memset) exists before capture.
+different streams get different ones.  A workspace is zero-filled by a kernel
+(never a memset) when it is allocated, also inside a graph capture, where the
+fill becomes part of the graph.  A workspace that a later, larger call
+supersedes is kept alive (never freed), because graphs captured before still
+write to it on every replay.
 """
 from __future__ import annotations
 
@@ -41,14 +43,26 @@ from . import kvq
 
 _ws_lock = threading.Lock()
 _workspaces: dict = {}
+# Superseded workspaces are kept, never freed: a graph captured from an earlier
+# call still writes its split records and arrival counters there on every
+# replay, and the caching allocator would otherwise hand that memory to other
+# tensors.  Growth at least doubles, so these hold fewer bytes than the live ones.
+_retired: list = []
 
 
 def _workspace(key, nbytes: int, device) -> Tensor:
     with _ws_lock:
         ws = _workspaces.get(key)
         if ws is None or ws.numel() < nbytes:
-            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
-            kvq.workspace_init(ws, nbytes)
+            # During a capture torch allocates from the graph's private pool
+            # and the zero-fill kernel is captured too (replays re-zero the
+            # counters, which every completed launch leaves at zero anyway).
+            size = max(nbytes, 2 * ws.numel() if ws is not None else 0, 1)
+            new = torch.empty(size, dtype=torch.uint8, device=device)
+            kvq.workspace_init(new, size)
+            if ws is not None:
+                _retired.append(ws)
+            ws = new
             _workspaces[key] = ws
         return ws
 

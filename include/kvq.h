@@ -48,9 +48,11 @@ extern "C" {
  * without device work (as KV_int8_split_optimized.cu:306-324).  Runs
  * asynchronously on the null stream.  Split workspace comes from a per-device
  * cache owned by the library (allocated on first use, grown when needed). */
+#ifndef KVQ_OMIT_DECODE_SOLVE /* defined by code that declares the attention `solve` (kvq_attention.h) */
 void solve(const float* Q, const int8_t* K_int8, const int8_t* V_int8,
            const float* k_scale, const float* v_scale, float* output,
            int num_heads, int seq_len, int head_dim);
+#endif
 
 /* Replaces `kv_int8_split_launch`, kv_cache/KV_int8_split_optimized.cu:266-292.
  * S is caller-owned scratch of at least num_heads*seq_len floats; it holds the
@@ -287,6 +289,52 @@ hipError_t kvq_attention_launch(const kvq_attention_params* p, void* workspace, 
 
 /* Library version string, e.g. "kvq 0.1.0 gfx950". */
 const char* kvq_version(void);
+
+/* ============ Part 6: plan queries and diagnostics (no counterpart in the reference) ============
+ *
+ * Host-only: these read no device memory and make no HIP call, so pointers
+ * may be any values with the alignment of the real ones.  They report what
+ * the matching launch would do. */
+
+#define KVQ_KERNEL_DECODE_GENERIC 0   /* decode_generic: any head dim or alignment */
+#define KVQ_KERNEL_DECODE_VALU 1      /* decode_fast: per-lane FMAs */
+#define KVQ_KERNEL_DECODE_MFMA 2      /* decode_mfma: grouped-query heads on matrix cores */
+#define KVQ_KERNEL_ATTENTION_MFMA 3   /* attention_mfma: query blocks on matrix cores */
+#define KVQ_KERNEL_ATTENTION_ROWS 4   /* attention_rows: up to 8 queries per workgroup */
+#define KVQ_KERNEL_ATTENTION_GENERIC 5 /* attention_generic: any head dim or alignment */
+
+#define KVQ_SPLITS_STATIC 0     /* splits and chunk fixed on the host */
+#define KVQ_SPLITS_IN_KERNEL 1  /* ragged batch planned inside the decode kernel */
+#define KVQ_SPLITS_SCHEDULE 2   /* ragged batch planned by a schedule launch */
+
+typedef struct kvq_plan_info {
+    int kernel;             /* KVQ_KERNEL_* */
+    int heads_per_group;    /* query heads one workgroup computes */
+    int splits;             /* static plans: splits per sequence (1 = unsplit); 0 otherwise */
+    int chunk;              /* static plans: tokens (keys) per split */
+    int split_plan;         /* KVQ_SPLITS_* */
+    int query_block;        /* attention: queries per workgroup; decode: 0 */
+    size_t workspace_bytes; /* workspace (or scratch S) bytes the launch uses */
+} kvq_plan_info;
+
+/* The plan of kv_int8_split_launch / kv_int8_simple_launch for these
+ * arguments; workspace_bytes is the part of S it uses (<= 4*num_heads*seq_len).
+ * hipErrorInvalidValue for arguments the launch rejects. */
+hipError_t kvq_reference_plan(const float* Q, const int8_t* K_int8, const int8_t* V_int8, int num_heads,
+                              int seq_len, int head_dim, kvq_plan_info* info);
+/* The plan of kvq_decode_launch for p. */
+hipError_t kvq_decode_plan(const kvq_decode_params* p, kvq_plan_info* info);
+/* The plan of kvq_attention_launch for p (attention_online_launch: p with
+ * softmax_scale 0 and num_splits 0). */
+hipError_t kvq_attention_plan(const kvq_attention_params* p, kvq_plan_info* info);
+
+/* Diagnostic switches in force, read once from the environment:
+ * bit 0: KVQ_DEBUG_SYNC ("1", "true", "yes" or "on"): every launching entry
+ *        point synchronises its stream after its launches and returns the first
+ *        error (not while the stream is being captured);
+ * bits 4-7: KVQ_FORCE_KERNEL: 1 = "valu" (decode plans avoid the matrix-core
+ *        kernel), 2 = "generic" (decode plans avoid both tuned kernels). */
+int kvq_diagnostics(void);
 
 #ifdef __cplusplus
 }

@@ -23,7 +23,8 @@ def test_bench_help_lists_options():
     r = _run("bench.py", "--help")
     assert r.returncode == 0
     for opt in ("--gpus", "--steps", "--warmup", "--settle-ms", "--config", "--splits", "--page-size",
-                "--page-order", "--seed", "--no-cpu", "--cpu-budget"):
+                "--page-order", "--seed", "--no-cpu", "--cpu-budget", "--configs", "--config-steps",
+                "--config-cpu-budget"):
         assert opt in r.stdout, opt
 
 
@@ -46,3 +47,21 @@ def test_traffic_summary_covers_the_decode_configs():
         assert e["hbm_bytes_per_launch"] == e["read_bytes_per_launch"] + e["write_bytes_per_launch"]
         assert 1.0 <= e["hbm_bytes_per_launch"] / e["algorithmic_bytes_per_launch"] < 1.03, cfg
         assert os.path.exists(os.path.join(REPO, e["source"]))
+
+
+def test_bench_helpers_without_gpu():
+    """The parity check and provenance helpers of bench.py on host data."""
+    import importlib.util
+    import numpy as np
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(REPO, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    ref = np.array([[1.0, -2.0, 0.0]], np.float32)
+    ok = bench.check_step(ref + np.float32(5e-5), ref)
+    assert ok["within_tolerance"] and 0.2 < ok["max_tol_frac"] < 0.6
+    bad = bench.check_step(ref + np.float32(1e-2), ref)
+    assert not bad["within_tolerance"] and bad["max_tol_frac"] > 1.0
+    nan = bench.check_step(np.full_like(ref, np.nan), ref)
+    assert nan["within_tolerance"] is False and nan["max_abs_err"] is None
+    hi = bench.host_info()
+    assert hi["nproc"] >= 1 and hi["os_cpu_count"] >= 1

@@ -328,3 +328,130 @@ int main() {
     subprocess.run(["g++", "-std=c++17", "-O2", "-I", csrc, str(src), "-o", str(exe)], check=True)
     r = subprocess.run([str(exe)], capture_output=True, text=True)
     assert r.returncode == 0 and r.stdout.strip().endswith("OK"), r.stdout[-2000:]
+
+
+STRUCTS["kvq_plan_info"] = kvq.PlanInfo
+
+
+@pytest.mark.parametrize("d", [32, 64, 96, 128, 256])
+def test_reference_plan_fits_caller_scratch(L, d):
+    """kv_int8_split_launch keeps every split record inside the caller's S
+    (H*N floats, kv_cache/KV_int8_split_optimized.cu:266-267), including the
+    padding between the (m, l) and accumulator regions: at d = 256, H = 1,
+    N = 516, N / (d + 2) = 2 splits would need 2304 bytes of a 2064-byte S."""
+    worst = 0.0
+    for H in (1, 2, 3, 5, 16, 256):
+        for N in list(range(1, 1100)) + [2047, 2048, 4096, 4097, 16384, 131072]:
+            info = kvq.reference_plan(H, N, d)
+            assert info.workspace_bytes <= 4 * H * N, (H, N, d, info.splits, info.workspace_bytes)
+            if info.splits > 1:
+                assert info.splits <= N // (d + 2)
+                worst = max(worst, info.workspace_bytes / (4 * H * N))
+            else:
+                assert info.workspace_bytes == 0
+    if d >= 96:
+        assert worst > 0.7  # the bound binds here, it is not met by never splitting
+    info = kvq.reference_plan(1, 516, 256)
+    assert info.splits == 1 and info.workspace_bytes == 0
+
+
+def test_plan_queries_reject_like_launches(L):
+    info = kvq.PlanInfo()
+    assert L.kvq_reference_plan(FAKE, FAKE, FAKE, 0, 4, 64, ctypes.byref(info)) == INVALID
+    assert L.kvq_reference_plan(None, FAKE, FAKE, 4, 4, 64, ctypes.byref(info)) == INVALID
+    assert L.kvq_reference_plan(FAKE, FAKE, FAKE, 4, 4, 64, None) == INVALID
+    p = kvq.DecodeParams(2, 8, 2, 128, 64, 64, None, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0.0, 0, None, None)
+    assert L.kvq_decode_plan(ctypes.byref(p), ctypes.byref(info)) == 0
+    p.num_q_heads = 7
+    assert L.kvq_decode_plan(ctypes.byref(p), ctypes.byref(info)) == INVALID
+    a = kvq.AttentionParams(4, 4, 0, FAKE, FAKE, FAKE, FAKE, 0.0, 0)
+    assert L.kvq_attention_plan(ctypes.byref(a), ctypes.byref(info)) == INVALID
+
+
+def test_decode_plan_kernels(L):
+    A = 1 << 20  # 16-byte aligned fake pointers
+
+    def plan(B, Hq, Hkv, d, cap, lengths=None, splits=0, misalign=0):
+        p = kvq.DecodeParams(B, Hq, Hkv, d, cap, 0 if lengths else cap, lengths, A + misalign, A, A, A, A, A,
+                             0.0, splits, None, None)
+        return kvq.decode_plan(p)
+
+    assert plan(8, 32, 32, 128, 4096).kernel == kvq.KERNEL_DECODE_VALU           # cfg1
+    i = plan(16, 32, 8, 128, 8192, lengths=A)                                    # cfg2
+    assert (i.kernel, i.heads_per_group, i.split_plan) == (kvq.KERNEL_DECODE_MFMA, 4, kvq.SPLITS_IN_KERNEL)
+    i = plan(1, 32, 8, 128, 131072)                                              # cfg3
+    assert (i.kernel, i.split_plan, i.splits) == (kvq.KERNEL_DECODE_MFMA, kvq.SPLITS_STATIC, 32)
+    i = plan(256, 64, 8, 128, 4096, lengths=A)                                   # cfg4
+    assert (i.kernel, i.heads_per_group, i.split_plan) == (kvq.KERNEL_DECODE_MFMA, 8, kvq.SPLITS_SCHEDULE)
+    assert plan(1, 8, 8, 64, 1024).splits == 1                                   # cfg0
+    assert plan(1, 8, 8, 96, 1024).kernel == kvq.KERNEL_DECODE_GENERIC
+    assert plan(1, 8, 8, 128, 1024, misalign=4).kernel == kvq.KERNEL_DECODE_GENERIC
+    assert plan(1, 4, 4, 128, 8192, splits=8).splits == 8
+
+
+def test_attention_plan_routes_misaligned_to_generic(L):
+    """Unaligned q/k/v/out at a tuned head dim take attention_generic, unsplit
+    (the tuned kernels use 16-byte vector accesses)."""
+    A = 1 << 20
+    for d in (32, 64, 128, 256):
+        for M, N in ((1, 65536), (6, 4096), (64, 4096), (1024, 1024)):
+            p = kvq.AttentionParams(M, N, d, A, A, A, A, 0.0, 0)
+            tuned = kvq.attention_plan(p)
+            assert tuned.kernel in (kvq.KERNEL_ATTENTION_ROWS, kvq.KERNEL_ATTENTION_MFMA)
+            assert tuned.kernel == (kvq.KERNEL_ATTENTION_ROWS if M <= 8 else kvq.KERNEL_ATTENTION_MFMA)
+            for which in range(4):
+                ptrs = [A, A, A, A]
+                ptrs[which] += 4
+                p = kvq.AttentionParams(M, N, d, *ptrs, 0.0, 0)
+                g = kvq.attention_plan(p)
+                assert (g.kernel, g.splits, g.workspace_bytes) == (kvq.KERNEL_ATTENTION_GENERIC, 1, 0)
+                assert L.kvq_attention_workspace_size(ctypes.byref(p)) == 0
+
+
+def _diagnostics_with(env_updates):
+    env = dict(os.environ)
+    env.pop("KVQ_DEBUG_SYNC", None)
+    env.pop("KVQ_FORCE_KERNEL", None)
+    env.update(env_updates)
+    code = ("import ctypes,sys; L=ctypes.CDLL(sys.argv[1]); L.kvq_diagnostics.restype=ctypes.c_int; "
+            "print(L.kvq_diagnostics())")
+    out = subprocess.run(["python3", "-c", code, kvq.LIB_PATH], env=env, capture_output=True, text=True,
+                         check=True)
+    return int(out.stdout.strip())
+
+
+@pytest.mark.parametrize("value,on", [("1", True), ("true", True), ("ON", True), ("yes", True), ("0", False),
+                                      ("", False), ("off", False), ("2", False), ("false", False)])
+def test_debug_sync_switch_parsing(value, on):
+    assert _diagnostics_with({"KVQ_DEBUG_SYNC": value}) & 1 == int(on)
+
+
+def test_force_kernel_switch(L):
+    assert _diagnostics_with({}) == 0
+    assert _diagnostics_with({"KVQ_FORCE_KERNEL": "valu"}) == 1 << 4
+    assert _diagnostics_with({"KVQ_FORCE_KERNEL": "generic"}) == 2 << 4
+    assert _diagnostics_with({"KVQ_FORCE_KERNEL": "mfma"}) == 0
+    # The forced plan itself: cfg2's shape on the per-lane FMA kernel.
+    env = dict(os.environ, KVQ_FORCE_KERNEL="valu", PYTHONPATH=REPO)
+    code = ("import importlib; k=importlib.import_module('cuda-operators_amd').kvq; A=1<<20; "
+            "p=k.DecodeParams(16,32,8,128,8192,0,A,A,A,A,A,A,A,0.0,0,None,None); i=k.decode_plan(p); "
+            "print(i.kernel, i.heads_per_group)")
+    out = subprocess.run(["python3", "-c", code], env=env, capture_output=True, text=True, check=True)
+    assert out.stdout.split() == [str(kvq.KERNEL_DECODE_VALU), "4"]
+
+
+def test_attention_compat_library_exports_solve():
+    """libkvq_attention.so exports exactly the `solve` include/kvq_attention.h
+    declares (attention/softmax_new.cu:283-287) and resolves
+    attention_online_launch from libkvq.so."""
+    hdr = os.path.join(REPO, "include", "kvq_attention.h")
+    text = re.sub(r"/\*.*?\*/", "", open(hdr).read(), flags=re.S)
+    assert set(re.findall(r"^\s*(?:[\w\s\*]+?)\b(\w+)\s*\(", text, flags=re.M)) == {"solve"}
+    nm = subprocess.run(["nm", "-D", "--defined-only", kvq.ATTN_LIB_PATH], capture_output=True, text=True,
+                        check=True)
+    assert {ln.split()[-1] for ln in nm.stdout.splitlines() if " T " in ln} == {"solve"}
+    und = subprocess.run(["nm", "-D", "--undefined-only", kvq.ATTN_LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    assert "attention_online_launch" in und
+    A = kvq.attention_lib()
+    assert A.solve is not kvq.lib().solve

@@ -55,12 +55,15 @@ def test_attention_few_queries(o, d, M, N):
 
 
 @pytest.mark.parametrize("splits", [1, 2, 5, 1 << 20])
-@pytest.mark.parametrize("d", [64, 128])
-def test_attention_few_queries_peaked_and_splits(o, d, splits):
+@pytest.mark.parametrize("M", [4, 6])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_attention_few_queries_peaked_and_splits(o, d, M, splits):
     """Large logits (frequent rescales) in the few-query kernel under any
-    split request, and identical keys (the output is the mean of V)."""
-    rng = np.random.default_rng(d + splits)
-    M, N = 6, 3000
+    split request, and identical keys (the output is the mean of V).  M = 4
+    runs the 4-query block, M = 6 the 8-query block; at d = 256 (and 128)
+    both spread a key row over d/8 lanes with 8 dims each."""
+    rng = np.random.default_rng(d + splits + 1000 * M)
+    N = 3000
     q, k, v = _problem(rng, M, N, d, qscale=8.0)
     gq, gk, gv = up(q), up(k), up(v)
     out = _gpu.poisoned((M, d))
@@ -103,18 +106,37 @@ def test_attention_online_generic_dims(o, d):
 
 
 @pytest.mark.parametrize("which", ["q", "k", "v", "out"])
-def test_attention_misaligned_takes_generic_path(o, which):
-    rng = np.random.default_rng(11)
-    M, N, d = 150, 333, 64
+@pytest.mark.parametrize("M,N,d", [(150, 333, 64), (4, 5000, 128), (1, 65536, 256), (300, 2000, 32)])
+def test_attention_misaligned_takes_generic_path(o, which, M, N, d):
+    """A 4-byte-aligned q, k, v or out at a tuned head dim runs
+    attention_generic, unsplit (kvq_attention_plan says so), and matches."""
+    rng = np.random.default_rng(11 + M + d)
     q, k, v = _problem(rng, M, N, d)
     t = {"q": up(q), "k": up(k), "v": up(v), "out": _gpu.poisoned((M, d))}
+    aligned = kvq.attention_plan(kvq.attention_params(t["q"], t["k"], t["v"], t["out"]))
+    assert aligned.kernel != kvq.KERNEL_ATTENTION_GENERIC
     base = torch.full((t[which].numel() + 1,), float("nan"), dtype=torch.float32, device="cuda")
     shifted = base[1:].view(t[which].shape)
     shifted.copy_(t[which])
     t[which] = shifted
+    info = kvq.attention_plan(kvq.attention_params(t["q"], t["k"], t["v"], t["out"]))
+    assert (info.kernel, info.splits, info.workspace_bytes) == (kvq.KERNEL_ATTENTION_GENERIC, 1, 0)
     kvq.attention_online(t["q"], t["k"], t["v"], t["out"])
     torch.cuda.synchronize()
     _close(down(t["out"]), o.attention_f32(q, k, v), which)
+
+
+@pytest.mark.parametrize("M,N,d", [(1, 65536, 128), (37, 301, 96), (200, 1000, 64)])
+def test_attention_compat_solve(o, M, N, d):
+    """The reference's `solve(Q, K, V, output, M, N, d)`
+    (attention/softmax_new.cu:283-287) from libkvq_attention.so: asynchronous
+    on the null stream, same result as attention_online_launch."""
+    rng = np.random.default_rng(M + N + d)
+    q, k, v = _problem(rng, M, N, d)
+    out = _gpu.poisoned((M, d))
+    kvq.attention_solve(up(q), up(k), up(v), out)
+    torch.cuda.synchronize()
+    _close(down(out), o.attention_f32(q, k, v), f"solve M={M} N={N} d={d}")
 
 
 @pytest.mark.parametrize("splits", [1, 2, 3, 7, 64, 1 << 20])

@@ -105,3 +105,48 @@ def test_solve_twice_reuses_workspace():
 
 def test_tolerance_constants():
     assert (ATOL, RTOL) == (1e-4, 1e-3)
+
+
+@pytest.mark.parametrize("H,N,d", [(1, 576, 256), (1, 516, 256), (16, 774, 256), (1, 769, 128), (1, 1025, 96)])
+def test_split_launch_stays_inside_scratch(H, N, d):
+    """kv_int8_split_launch writes only the first H*N floats of S: shapes where
+    the record layout fills S (or would overrun it without the bound) run with
+    a canary tail after S that must come back unchanged."""
+    info = kvq.reference_plan(H, N, d)
+    assert info.workspace_bytes <= 4 * H * N
+    rng = np.random.default_rng(H * 100000 + N * 10 + d)
+    Q, K, V, ks, vs = _gpu.reference_problem(H, N, d, rng)
+    want = orc.get().head_f32(Q, K, V, ks, vs)
+    gQ, gK, gV, gks, gvs = up(Q), up(K), up(V), up(ks), up(vs)
+    tail = 4096
+    buf = torch.full((H * N + tail,), float("nan"), dtype=torch.float32, device=_gpu.dev())
+    canary = torch.arange(tail, dtype=torch.float32, device=_gpu.dev()) * 0.5 + 12345.0
+    buf[H * N:] = canary
+    S = buf[: H * N]
+    for simple in (False, True):
+        out = poisoned((H, d))
+        assert kvq.kv_int8_split_launch(gQ, gK, gV, gks, gvs, out, S, simple=simple) == 0
+        torch.cuda.synchronize()
+        assert_close(down(out), want, what=f"H{H} N{N} d{d} splits {info.splits}")
+        assert torch.equal(buf[H * N:], canary), "kv_int8_split_launch wrote past S"
+
+
+SELFTEST_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "selftest")
+
+
+@pytest.mark.parametrize("argv", [[], ["8", "1024", "64"], ["3", "257", "128"], ["256", "4096", "128"],
+                                  ["2", "5000", "96"]], ids=lambda a: "x".join(a) or "default")
+def test_cpp_selftest_program(argv):
+    """The C++ self-test (tests/selftest/kvq_selftest.cpp) -- the reference's
+    main() of kv_cache/KV_int8_split_optimized.cu:439-543 on its patterned
+    inputs, linked against libkvq.so through include/kvq.h -- exits 0 after
+    solve, kv_int8_split_launch and kv_int8_simple_launch pass its 1e-4 gate."""
+    import subprocess
+    exe = os.path.join(SELFTEST_DIR, "kvq_selftest")
+    if not os.path.exists(exe):
+        subprocess.run(["make", "-C", SELFTEST_DIR, "all"], check=True, capture_output=True)
+    r = subprocess.run([exe, *argv], capture_output=True, text=True, timeout=120)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0, f"kvq_selftest {' '.join(argv)} exited {r.returncode}:\n{r.stdout}\n{r.stderr}"
+    for entry in ("solve", "kv_int8_split_launch", "kv_int8_simple_launch"):
+        assert entry in r.stdout, f"{entry} not exercised:\n{r.stdout}"

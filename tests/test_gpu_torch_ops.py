@@ -14,7 +14,7 @@ import _gpu
 from _gpu import down, kvq, up
 from oracle import oracle as orc
 
-importlib.import_module("cuda-operators_amd.torch_ops")
+torch_ops = importlib.import_module("cuda-operators_amd.torch_ops")
 pytestmark = pytest.mark.gpu
 
 
@@ -166,3 +166,48 @@ def test_attention_graph_capture_replays(o):
         eager = torch.ops.kvq.attention(g[0], g[1], g[2], 0.0, 0)
         torch.cuda.synchronize()
         assert np.array_equal(_bits(down(out)), _bits(down(eager))), f"replay {rep}"
+
+
+def test_graph_replay_after_workspace_growth(o):
+    """Capture a split decode step on stream s, then run a larger eager
+    problem on s (its workspace grows), then replay: the graph still owns
+    the workspace it was captured with (the superseded one is kept, not
+    freed), so the replay is correct and tensors allocated after the growth
+    are not overwritten."""
+    rng = np.random.default_rng(77)
+    Hkv, G, d = 2, 4, 128
+    B1, cap1 = 4, 1024
+    lengths = np.array([1024, 517, 33, 800], np.int32)
+    p = make_problem(rng, B1, Hkv * G, Hkv, cap1, d, o.quantize_rows, lengths=lengths)
+    g = [up(x) for x in (p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths)]
+    args = lambda: (g[0], g[1], g[2], g[3], g[4], g[5], cap1, 0.0, 0, None, None)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        torch.ops.kvq.decode(*args())
+    s.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out = torch.ops.kvq.decode(*args())
+    # A larger problem on the same stream grows the cached workspace (200
+    # sequences: the split-schedule plan, 2.2 MB against 0.8 MB).
+    B2, cap2 = 200, 1024
+    l2 = rng.integers(1, cap2 + 1, B2).astype(np.int32)
+    p2 = make_problem(rng, B2, Hkv * G, Hkv, cap2, d, o.quantize_rows, lengths=l2)
+    g2 = [up(x) for x in (p2["q"], p2["k"], p2["v"], p2["ks"], p2["vs"], l2)]
+    with torch.cuda.stream(s):
+        big = torch.ops.kvq.decode(g2[0], g2[1], g2[2], g2[3], g2[4], g2[5], cap2, 0.0, 0, None, None)
+    s.synchronize()
+    key = ("decode", 0, s.cuda_stream)
+    assert torch_ops._workspaces[key].numel() >= 2179840 and len(torch_ops._retired) >= 1
+    np.testing.assert_allclose(down(big), o.decode_f32(p2["q"], p2["k"], p2["v"], p2["ks"], p2["vs"], lengths=l2),
+                               atol=1e-4, rtol=1e-3)
+    guards = [torch.full((794624 // 4,), 7.0, device="cuda") for _ in range(16)]  # the old workspace's size
+    for rep in range(3):
+        g[0].copy_(up(rng.standard_normal(p["q"].shape).astype(np.float32)))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = o.decode_f32(down(g[0]), p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+        np.testing.assert_allclose(down(out), want, atol=1e-4, rtol=1e-3, err_msg=f"replay {rep}")
+        assert all(bool((t == 7.0).all()) for t in guards), f"replay {rep} wrote into freed memory"
