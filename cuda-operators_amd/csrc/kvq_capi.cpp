@@ -416,6 +416,37 @@ hipError_t decode_run(const kvq_decode_params* p, const DecodePlan& plan, void* 
     return kvq::launch_decode(a, plan, stream);
 }
 
+// Workspace of kvq_decode_launch_noalloc: a fixed device array in place of a
+// caller's allocation.  Each GPU holds its own copy at its own address until
+// the process ends; the host name `scratch` is not a device address, so the
+// address is looked up once per device (hipGetSymbolAddress, with that device
+// current) and only that pointer is ever passed to kernels.  The arrival
+// counters at its start are zero-filled (by a kernel) on the first call on
+// each device; every completed launch leaves them at zero again, as for any
+// workspace.  All calls on one GPU share the array, so calls that overlap in
+// time on one GPU race.
+static __device__ __align__(256) unsigned char scratch[KVQ_NOALLOC_SCRATCH_BYTES];
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[64];
+
+hipError_t noalloc_scratch(hipStream_t stream, void** out) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return err;
+        if (ptr == nullptr) return hipErrorInvalidSymbol;
+        err = kvq::launch_fill_zero(ptr, kCounterBytes, stream);
+        if (err != hipSuccess) return err;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
 
 bool decode_aligned(const kvq_decode_params* p) {
     return aligned16(p->q) && aligned16(p->k_cache) && aligned16(p->v_cache) && (p->head_dim % 16) == 0 &&
@@ -678,6 +709,19 @@ hipError_t kvq_decode_launch(const kvq_decode_params* p, void* workspace, size_t
     const size_t need = plan_bytes(plan);
     if (need > 0 && (!workspace || workspace_bytes < need)) return hipErrorInvalidValue;
     return finish_call(decode_run(p, plan, workspace, stream), stream);
+}
+
+hipError_t kvq_decode_launch_noalloc(const kvq_decode_params* p, hipStream_t stream) {
+    if (!decode_params_ok(p)) return hipErrorInvalidValue;
+    const DecodePlan plan = decode_plan(p);
+    const size_t need = plan_bytes(plan);
+    if (need > KVQ_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;  // beyond the fixed scratch array
+    void* ws = nullptr;
+    if (need > 0) {
+        const hipError_t err = noalloc_scratch(stream, &ws);
+        if (err != hipSuccess) return err;
+    }
+    return finish_call(decode_run(p, plan, ws, stream), stream);
 }
 
 hipError_t kvq_append_launch(const kvq_append_params* p, hipStream_t stream) {

@@ -118,7 +118,7 @@ EXPORTS = ("solve", "kv_int8_split_launch", "kv_int8_simple_launch", "kvq_decode
            "kvq_paged_decode_workspace_size", "kvq_paged_decode_launch", "kvq_paged_append_launch",
            "kvq_prefill_quantize_launch", "attention_online_launch", "kvq_attention_workspace_size",
            "kvq_attention_launch", "kvq_version", "kvq_reference_plan", "kvq_decode_plan", "kvq_attention_plan",
-           "kvq_diagnostics")
+           "kvq_diagnostics", "kvq_decode_launch_noalloc")
 
 
 class KvqError(RuntimeError):
@@ -148,6 +148,8 @@ def lib() -> ctypes.CDLL:
         L.kvq_workspace_init.restype = _int
         L.kvq_decode_launch.argtypes = [ctypes.POINTER(DecodeParams), _vp, ctypes.c_size_t, _vp]
         L.kvq_decode_launch.restype = _int
+        L.kvq_decode_launch_noalloc.argtypes = [ctypes.POINTER(DecodeParams), _vp]
+        L.kvq_decode_launch_noalloc.restype = _int
         L.kvq_append_launch.argtypes = [ctypes.POINTER(AppendParams), _vp]
         L.kvq_append_launch.restype = _int
         L.kvq_quantize_rows_launch.argtypes = [_vp, ctypes.c_int64, _int, _vp, _vp, _vp]
@@ -279,6 +281,15 @@ def new_workspace(p: DecodeParams, device=None, stream=None) -> torch.Tensor:
 def decode_launch(p: DecodeParams, ws, stream=None) -> None:
     nbytes = 0 if ws is None else ws.numel() * ws.element_size()
     _check("kvq_decode_launch", lib().kvq_decode_launch(ctypes.byref(p), _ptr(ws), nbytes, _stream(stream)))
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20  # KVQ_NOALLOC_SCRATCH_BYTES
+
+
+def decode_launch_noalloc(p: DecodeParams, stream=None) -> int:
+    """kvq_decode_launch_noalloc: the library's fixed device scratch array in
+    place of a workspace (allocates nothing).  Returns the hipError code."""
+    return int(lib().kvq_decode_launch_noalloc(ctypes.byref(p), _stream(stream)))
 
 
 class Decoder:
@@ -535,4 +546,4 @@ __all__ = ["lib", "version", "solve", "kv_int8_split_launch", "DecodeParams", "A
            "PagedAppendParams", "PagedDecoder", "paged_append", "PrefillParams", "prefill", "DTYPE_F32",
            "DTYPE_BF16", "AttentionParams", "attention_online", "attention_params", "attention_workspace_size",
            "attention", "PlanInfo", "reference_plan", "decode_plan", "attention_plan", "diagnostics",
-           "attention_lib", "attention_solve"]
+           "attention_lib", "attention_solve", "decode_launch_noalloc", "NOALLOC_SCRATCH_BYTES"]

@@ -122,6 +122,22 @@ hipError_t kvq_workspace_init(void* workspace, size_t workspace_bytes, hipStream
 hipError_t kvq_decode_launch(const kvq_decode_params* p, void* workspace, size_t workspace_bytes,
                              hipStream_t stream);
 
+/* Size of the fixed device scratch array of kvq_decode_launch_noalloc. */
+#define KVQ_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* No counterpart in the reference.  kvq_decode_launch without a workspace
+ * argument and without any allocation, for callers that cannot allocate device
+ * memory (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The split records and arrival counters live in a fixed
+ * KVQ_NOALLOC_SCRATCH_BYTES device array that each GPU holds until the process
+ * ends (its counters are zero-filled by a kernel on the first call on each
+ * device and left at zero by every completed launch).  Same plan, kernels and
+ * result bits as kvq_decode_launch.  hipErrorInvalidValue for the arguments
+ * kvq_decode_launch rejects and when kvq_decode_workspace_size(p) exceeds
+ * KVQ_NOALLOC_SCRATCH_BYTES.  All calls on one GPU share the array: calls that
+ * overlap in time on one GPU (different streams, or host threads) race. */
+hipError_t kvq_decode_launch_noalloc(const kvq_decode_params* p, hipStream_t stream);
+
 typedef struct kvq_append_params {
     int batch, num_kv_heads, head_dim, capacity;
     const int32_t* positions; /* device [B] write position per sequence, or NULL */
