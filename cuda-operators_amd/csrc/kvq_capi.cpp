@@ -102,6 +102,16 @@ bool debug_sync() {
 
 enum ForcedKernel { kForceNone = 0, kForceValu = 1, kForceGeneric = 2 };
 
+// KVQ_FLAT_PLAN=0 keeps ragged matrix-core batches on the per-sequence item
+// plan (locate_fit), for comparison.
+bool flat_enabled() {
+    static const bool on = [] {
+        const char* s = getenv("KVQ_FLAT_PLAN");
+        return !(s && strcmp(s, "0") == 0);
+    }();
+    return on;
+}
+
 int forced_kernel() {
     static const int k = [] {
         const char* s = getenv("KVQ_FORCE_KERNEL");
@@ -168,6 +178,31 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
     const int U = Hkv * p.nsg;
     const bool fit_kernel = p.kernel == kvq::Kernel::Mfma || (p.kernel == kvq::Kernel::Valu && p.sg <= 2);
     const int fit_items = (p.kernel == kvq::Kernel::Mfma ? KVQ_FIT_TARGET_MFMA : KVQ_FIT_TARGET_VALU) / U;
+    if (ragged && requested == 0 && fused && p.kernel == kvq::Kernel::Mfma && fit_items >= 1 &&
+        B <= kvq::kFitMaxSeqs && 4 * B >= fit_items && static_cast<long>(B) * U <= kMaxCounters &&
+        max_len <= (1 << 30) && flat_enabled()) {
+        // Ragged batch of at most 64 sequences on the matrix cores: the
+        // workgroups' waves take equal ranges of the sequences' tiles laid end
+        // to end (decode_mfma_flat).  A sequence covering w waves is merged
+        // from w records by one wave, so batches with over 16 waves per
+        // sequence on average (4 * fit_items waves, B < fit_items / 4) keep
+        // the per-sequence item plan below (two sequences of 30-60K tokens:
+        // 53 us flat, 42 us itemised; B = 8, 4K-32K tokens: 57 / 56 us;
+        // B = 16, cfg2: 33.1 / 34.0 us).  Record ids run to waves + B per
+        // query head.
+        p.fit = true;
+        p.flat = true;
+        p.counters = true;
+        p.sched_items = fit_items;
+        p.sched_gran = gran;
+        p.splits = 0;
+        p.chunk = 0;
+        const size_t recs = (static_cast<size_t>(fit_items) * kvq::kMfmaWaves + B) * Hq;
+        p.counter_bytes = kCounterBytes;
+        p.ml_bytes = round_up(recs * 2 * sizeof(float), kAlign);
+        p.acc_bytes = round_up(recs * static_cast<size_t>(d) * sizeof(float), kAlign);
+        return p;
+    }
     if (ragged && requested == 0 && fused && fit_kernel && units <= kMaxCounters && B <= kvq::kFitMaxSeqs &&
         B <= fit_items && max_len <= (1 << 30)) {
         // Small ragged batch: every workgroup plans the batch itself from the
@@ -253,6 +288,7 @@ void bind_workspace(DecodeArgs& a, const DecodePlan& p, void* ws) {
     a.sched = p.scheduled ? reinterpret_cast<const int*>(base + p.counter_bytes) : nullptr;
     a.sched_items = p.sched_items;
     a.fit_items = p.fit ? p.sched_items : 0;
+    a.flat = p.flat ? 1 : 0;
     a.fit_gran = p.sched_gran;
     const size_t ml = p.counter_bytes + p.sched_bytes;
     a.part_ml = p.ml_bytes ? reinterpret_cast<float*>(base + ml) : nullptr;

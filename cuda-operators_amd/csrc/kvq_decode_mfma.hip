@@ -51,7 +51,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
-constexpr int kMWaves = 4;        // waves per workgroup
+constexpr int kMWaves = kMfmaWaves;  // waves per workgroup
 constexpr int kMTile = 32;        // tokens per wave tile
 constexpr float kPScale = 32768.0f;  // PV weights are formed in [-2^15, 2^15] before the f16 split
 constexpr int kMBStep = kMTile * kMWaves;
@@ -515,6 +515,626 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     finish_split<true>(a, unit, map, bhq0, G, nsplit, &s_last);
 }
 
+
+// ---------------------------------------------------------------------------
+// decode_mfma_flat: a ragged batch of at most kFitMaxSeqs sequences, balanced
+// over waves rather than over whole work items.
+//
+// For one work unit (kv head, head group) the sequences' 32-token tiles are
+// laid end to end: sequence b owns tiles [E_b, E_b + n_b), n_b = ceil(len_b /
+// 32), T tiles in all.  The W = 4 * fit_items waves of the unit's workgroups
+// take equal contiguous ranges of that stream (tile counts differ by at most
+// one), whatever the lengths, where a plan of whole items per sequence waits
+// for its largest item (cfg2: 1.26-1.36x the mean).  A wave's range may cross
+// sequence boundaries: the tile loads run one tile ahead across the switch
+// (the next sequence's q limbs are loaded with its first tile), so a switch
+// costs no pipeline drain.  Per wave:
+// * a middle segment (a whole sequence) writes its output directly;
+// * a first segment that ends inside the range (the tail of a sequence begun
+//   by earlier waves) writes a partial record with record id gw + b;
+// * the last segment stays in registers.  At the end the workgroup's waves
+//   whose last segments share a sequence (a run of consecutive waves) combine
+//   through LDS into one output or one record (id of the run's first wave + b).
+// Record ids gw + b are distinct for distinct (wave, sequence) pairs because
+// both grow along the stream.  Arrivals are counted in waves: a record adds
+// the number of waves it stands for, and the arrival that completes the count
+// of waves covering b (known from the plan) merges b's records: one per
+// workgroup whose waves end in b, plus the tail record of the wave in which b
+// ends, all located from the plan (merge_runs).  Every wave computes the same
+// plan from the device lengths with lane operations (lane b holds sequence b).
+// ---------------------------------------------------------------------------
+
+// A stream of T tiles over W waves: with q = T / W and r = T % W, wave j
+// takes q + 1 tiles if j < r, else q, starting at tile j * q + min(j, r)
+// (32-bit arithmetic only).  With T < W the first T waves take one tile each,
+// so every wave of a covering range holds tiles.
+struct FlatSplit {
+    int q, r;
+};
+__device__ __forceinline__ FlatSplit flat_split(int T, int W) {
+    const unsigned q = static_cast<unsigned>(T) / static_cast<unsigned>(W);
+    return {static_cast<int>(q), T - static_cast<int>(q) * W};
+}
+__device__ __forceinline__ int flat_start(const FlatSplit& f, int j) { return j * f.q + min(j, f.r); }
+__device__ __forceinline__ int flat_wave_of(const FlatSplit& f, int t) {  // the wave holding tile t < T
+    const int big = f.r * (f.q + 1);  // tiles of the waves that take q + 1
+    if (t < big) return static_cast<int>(static_cast<unsigned>(t) / static_cast<unsigned>(f.q + 1));
+    return f.r + static_cast<int>(static_cast<unsigned>(t - big) / static_cast<unsigned>(f.q));
+}
+
+// Log-sum-exp merge, by one wave, of sequence b's records for query heads
+// hq0 .. + G - 1 under the flattened plan: one record per wave covering b,
+// ids w0 + b .. w0 + b + nrec - 1, record id r of head hq at row r * Hq + hq.
+// kWave / G lanes per head, each with D / 4 / (kWave / G) 16-byte columns:
+// a record's (m, l) load serves all of a lane's columns, and KR records per
+// round are loaded together with device-coherent buffer loads.
+template <int D, int G>
+__device__ inline void merge_wave_records(const DecodeArgs& a, int b, int w0, int nrec, int hq0, int lane) {
+    constexpr int LPH = kWave / G;        // lanes per head
+    constexpr int NC = D / 4 / LPH;       // 16-byte columns per lane
+    constexpr int KR = NC <= 2 ? 16 : 8;  // records per round
+    const int h = lane / LPH;
+    const int c0 = lane - h * LPH;        // columns c0, c0 + LPH, ...
+    const size_t r0 = (static_cast<size_t>(w0) + b) * a.Hq + hq0;
+    const unsigned span = static_cast<unsigned>((nrec - 1) * a.Hq + G);
+    const buf_rsrc mlr = make_rsrc(a.part_ml + r0 * 2, span * 8u);
+    const buf_rsrc accr = make_rsrc(a.part_acc + r0 * D, span * static_cast<unsigned>(D) * 4u);
+    typedef int v2i_t __attribute__((ext_vector_type(2)));
+    float M = -INFINITY, L = 0.0f;
+    f32x4 A[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) A[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < nrec; k0 += KR) {
+        v2i_t ml[KR];
+        v4i_t acc[KR][NC];
+#pragma unroll
+        for (int k = 0; k < KR; k++) {
+            if (k0 + k < nrec) {
+                const int rec = (k0 + k) * a.Hq + h;
+                ml[k] = __builtin_amdgcn_raw_buffer_load_b64(mlr, rec * 8, 0, kCoherent);
+#pragma unroll
+                for (int j = 0; j < NC; j++)
+                    acc[k][j] = __builtin_amdgcn_raw_buffer_load_b128(accr, (rec * D + 4 * (c0 + j * LPH)) * 4, 0,
+                                                                      kCoherent);
+            }
+        }
+        float cm = M;
+#pragma unroll
+        for (int k = 0; k < KR; k++)
+            if (k0 + k < nrec) cm = fmaxf(cm, __int_as_float(ml[k].x));
+        const float f = fast_exp2(M - cm);  // 0 on the first round (M = -inf); every record is finite
+        L *= f;
+#pragma unroll
+        for (int j = 0; j < NC; j++) A[j] *= f;
+        M = cm;
+#pragma unroll
+        for (int k = 0; k < KR; k++) {
+            if (k0 + k < nrec) {
+                const float w = fast_exp2(__int_as_float(ml[k].x) - cm);
+                L = fmaf(__int_as_float(ml[k].y), w, L);
+#pragma unroll
+                for (int j = 0; j < NC; j++) A[j] += __builtin_bit_cast(f32x4, acc[k][j]) * w;
+            }
+        }
+    }
+    const float rl = 1.0f / L;
+    float* o = a.out + (static_cast<size_t>(b) * a.Hq + hq0 + h) * D;
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[4 * (c0 + j * LPH) + i] = A[j][i] * rl;
+    }
+}
+
+template <int D, int G, bool PAGED, bool APPEND>
+__global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(APPEND ? 1 : 2, APPEND ? 1 : 2))) void decode_mfma_flat(
+    const DecodeArgs a) {
+    static_assert(G == 4 || G == 8, "heads per workgroup");
+    static_assert(D == 64 || D == 128, "head dims of the matrix-core decode kernel");
+    constexpr int NJ = D / 64;
+    constexpr int NB = D / 16;
+    constexpr int RPLV = kWave / NB;
+    constexpr int NV = kMTile / RPLV;
+    constexpr int NE = 2 * D / kWave;
+    __shared__ __align__(16) int8_t s_v[kMWaves][2][kMTile * D];  // V tiles, per wave
+    __shared__ __align__(16) int8_t s_newq[kMWaves][2][D];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+
+    const int U = a.Hkv * a.nsg;
+    const int item = blockIdx.x / U;
+    const int unit = blockIdx.x - item * U;
+    const int kvh = unit / a.nsg;
+    const int sgi = unit - kvh * a.nsg;
+    const int hq0 = kvh * a.G + sgi * G;
+    const int Wn = a.fit_items * kMWaves;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int gw = item * kMWaves + wv;
+
+    // The plan: lane b holds sequence b's length, tiles and first tile.
+    const int B = a.B;
+    const int len_l = lane < B ? seq_len_of(a, lane) : 0;
+    const int n_l = (len_l + kMTile - 1) / kMTile;
+    int incl = n_l;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int y = __shfl_up(incl, off);
+        if (lane >= off) incl += y;
+    }
+    const int e_l = incl - n_l;
+    const int T = __builtin_amdgcn_readlane(incl, kWave - 1);
+    const FlatSplit fs = flat_split(T, Wn);
+    const int tb = flat_start(fs, gw);
+    const int te = flat_start(fs, gw + 1);
+    auto seq_of = [&](int t) {  // the sequence holding tile t < T
+        return static_cast<int>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < B && e_l <= t))) - 1;
+    };
+
+    // Zero rows of empty sequences, once per work unit.
+    if (item == 0 && wv == 0) {
+        unsigned long long empty = __builtin_amdgcn_ballot_w64(lane < B && len_l == 0);
+        while (empty) {
+            const int b = __builtin_ctzll(empty);
+            empty &= empty - 1;
+            for (int i = lane; i < G * D; i += kWave) a.out[(static_cast<size_t>(b) * a.Hq + hq0) * D + i] = 0.0f;
+        }
+    }
+
+    constexpr bool app = APPEND;  // a.k_new != nullptr
+    // q of head (r % G) of sequence b, dims 16g.. of each 64-dim block.
+    const int hrow = r % G;
+    float qv[16 * NJ];
+    auto load_q = [&](int b) {
+        const float* qp = a.q + (static_cast<size_t>(b) * a.Hq + hq0 + hrow) * D + 16 * g;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+#pragma unroll
+            for (int i4 = 0; i4 < 4; i4++) {
+                const float4 x = *reinterpret_cast<const float4*>(qp + 64 * j + 4 * i4);
+                qv[16 * j + 4 * i4] = x.x;
+                qv[16 * j + 4 * i4 + 1] = x.y;
+                qv[16 * j + 4 * i4 + 2] = x.z;
+                qv[16 * j + 4 * i4 + 3] = x.w;
+            }
+        }
+    };
+    i32x4 qb[NJ][3];
+    float qs = 0.0f;
+    auto prepare_q = [&]() {
+        float qmax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16 * NJ; i++) qmax = fmaxf(qmax, fabsf(qv[i]));
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 16));
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+        int qexp = 0;
+        frexpf(qmax, &qexp);
+        const int E = qmax > 0.0f ? min(max(22 - qexp, -100), 126) : 0;
+        qs = ldexpf(1.0f, -E) * a.scale_log2;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            int limb[3][16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int Q = static_cast<int>(__builtin_rintf(ldexpf(qv[16 * j + i], E)));
+                const int l2 = ((Q + 128) & 255) - 128;
+                const int Q1 = (Q - l2) >> 8;
+                const int l1 = ((Q1 + 128) & 255) - 128;
+                limb[0][i] = (Q1 - l1) >> 8;
+                limb[1][i] = l1;
+                limb[2][i] = l2;
+            }
+#pragma unroll
+            for (int lb = 0; lb < 3; lb++)
+                qb[j][lb] = i32x4{pack_bytes(&limb[lb][0]), pack_bytes(&limb[lb][4]), pack_bytes(&limb[lb][8]),
+                                  pack_bytes(&limb[lb][12])};
+        }
+    };
+
+    float m = -INFINITY, lsum = 0.0f, vref = 0.0f;
+    f32x4 acc[NB];
+#pragma unroll
+    for (int c = 0; c < NB; c++) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const bool lo_row = ((r / G) & 1) != 0;
+    const int rr = (lane & 15) >> 1;
+    const int h2 = lane & 1;
+    const int vrow = rr < 4 ? 4 * g + rr : 16 + 4 * g + (rr - 4);
+    const unsigned cap = static_cast<unsigned>(a.cap);
+
+    struct Tile {
+        i32x4 ka[2][NJ];
+        int4 v[NV];
+        float ks[2][4], vs[2][4];
+    };
+    const int kvo = r * D + 16 * g;
+    const int vvo = (lane / NB) * D + 16 * (lane % NB);
+    const int svo = 16 * g;
+    // Tile loads of sequence b at token `base` (a multiple of 32).  `none`:
+    // past the wave's range -- the same loads through empty resources (they
+    // read zeros and touch no memory), so that every iteration issues the
+    // same loads and the waits for the current tile can leave the next one in
+    // flight.
+    // The load cursor's sequence as buffer resources (contiguous layout;
+    // rebuilt only when the cursor moves to another sequence).
+    buf_rsrc lkr, lvr, lksr, lvsr;
+    auto set_load_seq = [&](int b) {
+        if constexpr (!PAGED) {
+            const size_t row0 = (static_cast<size_t>(b) * a.Hkv + kvh) * a.cap;
+            lkr = make_rsrc(a.k + row0 * D, cap * D);
+            lvr = make_rsrc(a.v + row0 * D, cap * D);
+            lksr = make_rsrc(a.ks + row0, cap * 4u);
+            lvsr = make_rsrc(a.vs + row0, cap * 4u);
+        }
+    };
+    auto load_tile = [&](Tile& Tt, int b, int base, bool none) {
+        buf_rsrc kr, vr, ksr, vsr;
+        int ko, so;
+        if (none) {
+            kr = vr = ksr = vsr = make_rsrc(a.k, 0u);
+            ko = so = 0;
+        } else if constexpr (PAGED) {
+            const size_t rp = cache_row(a.pages, a.Hkv, a.cap, b, kvh, base);
+            const unsigned rem = static_cast<unsigned>(a.pages.size - (base & (a.pages.size - 1)));
+            kr = make_rsrc(a.k + rp * D, rem * D);
+            vr = make_rsrc(a.v + rp * D, rem * D);
+            ksr = make_rsrc(a.ks + rp, rem * 4u);
+            vsr = make_rsrc(a.vs + rp, rem * 4u);
+            ko = so = 0;
+        } else {
+            kr = lkr;
+            vr = lvr;
+            ksr = lksr;
+            vsr = lvsr;
+            ko = base * D;
+            so = base * 4;
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+#pragma unroll
+            for (int j = 0; j < NJ; j++) Tt.ka[s][j] = buffer_load16_stream(kr, kvo + s * 16 * D + 64 * j, ko);
+        }
+#pragma unroll
+        for (int c = 0; c < NV; c++) {
+            const v4i_t x = buffer_load16_stream(vr, vvo + c * RPLV * D, ko);
+            Tt.v[c] = make_int4(x.x, x.y, x.z, x.w);
+        }
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const v4i_t xk = buffer_load16(ksr, svo + 64 * s, so);
+            const v4i_t xv = buffer_load16(vsr, svo + 64 * s, so);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                Tt.ks[s][i] = __int_as_float(xk[i]);
+                Tt.vs[s][i] = __int_as_float(xv[i]);
+            }
+        }
+    };
+    auto stage_v = [&](const Tile& Tt, int8_t* vt) {
+#pragma unroll
+        for (int c = 0; c < NV; c++) {
+            const int rw = RPLV * c + lane / NB;
+            const int p = lane % NB;
+            *reinterpret_cast<int4*>(vt + rw * D + (v_slot<D>(p, rw) << 4)) = Tt.v[c];
+        }
+    };
+
+    // Fused append of sequence b's token len-1 (its last tile is in this
+    // wave's range): the fp32 rows are loaded one tile ahead, quantised with
+    // the rule and bits of append_kernel, written to the cache once per kv head
+    // and substituted into the tile.
+    // Two banks: the next sequence's row may be loaded in the step that
+    // appends the current one (a one-tile sequence after a sequence end).
+    float xnew0[NE], xnew1[NE];
+    int x_issue = 0, x_use = 0;  // rows loaded / appended so far (bank = count & 1)
+    float newks = 0.0f, newvs = 0.0f;
+    auto load_new = [&](int b) {
+        const size_t bh = static_cast<size_t>(b) * a.Hkv + kvh;
+        if (x_issue & 1) {
+#pragma unroll
+            for (int j = 0; j < NE; j++)
+                xnew1[j] = (j < NJ ? a.k_new : a.v_new)[bh * D + ((lane + kWave * j) & (D - 1))];
+        } else {
+#pragma unroll
+            for (int j = 0; j < NE; j++)
+                xnew0[j] = (j < NJ ? a.k_new : a.v_new)[bh * D + ((lane + kWave * j) & (D - 1))];
+        }
+        x_issue++;
+    };
+    auto append_new = [&](int b, int tnew) {
+        float xnew[NE];
+#pragma unroll
+        for (int j = 0; j < NE; j++) xnew[j] = (x_use & 1) ? xnew1[j] : xnew0[j];
+        x_use++;
+        const size_t rnew = cache_row(a.pages, a.Hkv, a.cap, b, kvh, tnew);
+        float amk = fabsf(xnew[0]), amv = fabsf(xnew[NJ]);
+#pragma unroll
+        for (int j = 1; j < NJ; j++) {
+            amk = fmaxf(amk, fabsf(xnew[j]));
+            amv = fmaxf(amv, fabsf(xnew[NJ + j]));
+        }
+        newks = quant_scale(wave_max(amk));
+        newvs = quant_scale(wave_max(amv));
+#pragma unroll
+        for (int j = 0; j < NE; j++)
+            s_newq[wv][j / NJ][lane + kWave * (j % NJ)] =
+                static_cast<int8_t>(quant_one(xnew[j], j < NJ ? newks : newvs));
+        if (sgi == 0) {
+            if (lane < 2 * NB) {
+                const int row = lane / NB, piece = lane % NB;
+                *reinterpret_cast<int4*>((row ? a.v : a.k) + rnew * D + 16 * piece) =
+                    *reinterpret_cast<const int4*>(&s_newq[wv][row][16 * piece]);
+            }
+            if (lane == 0) {
+                a.ks[rnew] = newks;
+                a.vs[rnew] = newvs;
+            }
+        }
+    };
+    auto substitute_new = [&](Tile& Tt, int base, int tnew, int8_t* vt) {
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            if (base + 16 * s + r == tnew) {
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+                    Tt.ka[s][j] = *reinterpret_cast<const i32x4*>(&s_newq[wv][0][64 * j + 16 * g]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (base + 16 * s + 4 * g + i == tnew) {
+                    Tt.ks[s][i] = newks;
+                    Tt.vs[s][i] = newvs;
+                }
+        }
+        const int rw = tnew - base;
+        if (rw >= 0 && rw < kMTile && lane < NB)
+            *reinterpret_cast<int4*>(vt + rw * D + (v_slot<D>(lane, rw) << 4)) =
+                *reinterpret_cast<const int4*>(&s_newq[wv][1][16 * lane]);
+    };
+
+    // One tile of the current sequence (tokens [base, base + 32) of len).
+    auto compute = [&](const Tile& Tt, int base, int len, const int8_t* vt) {
+        i32x4 cq[2][3];
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+#pragma unroll
+            for (int lb = 0; lb < 3; lb++) {
+                i32x4 c = i32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < NJ; j++) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(Tt.ka[s][j], qb[j][lb], c, 0, 0, 0);
+                cq[s][lb] = c;
+            }
+        }
+        float sc[8], vsv[8];
+        float mt = -INFINITY, vmax = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int low = (cq[s][1][i] << 8) + cq[s][2][i];
+                const float dot = static_cast<float>(cq[s][0][i]) * 65536.0f + static_cast<float>(low);
+                sc[4 * s + i] = (dot * Tt.ks[s][i]) * qs;
+                vsv[4 * s + i] = Tt.vs[s][i];
+            }
+        }
+        if (base + kMTile > len) {
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (base + 16 * s + 4 * g + i >= len) {
+                        sc[4 * s + i] = -INFINITY;
+                        vsv[4 * s + i] = 0.0f;
+                    }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            mt = fmaxf(mt, sc[k]);
+            vmax = fmaxf(vmax, fabsf(vsv[k]));
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        vmax = fmaxf(vmax, __shfl_xor(vmax, 16));
+        vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
+        const float mn = fmaxf(m, mt);
+        const float ms = mn == -INFINITY ? 0.0f : mn;
+        const float alpha = fast_exp2(m - ms);
+        const float vn = fmaxf(vref, vmax);
+        const float rvn = vn > 0.0f ? __builtin_amdgcn_rcpf(vn) : 0.0f;
+        const float f = vn > 0.0f ? alpha * (vref * rvn) : alpha;
+        const float winv = kPScale * rvn;
+        m = mn;
+        vref = vn;
+        if (__builtin_amdgcn_ballot_w64(f != 1.0f) != 0) {
+#pragma unroll
+            for (int c = 0; c < NB; c++) acc[c] *= f;
+        }
+        float ps = 0.0f;
+        f16x8 pb;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float p = fast_exp2(sc[k] - ms);
+            ps += p;
+            const float w = p * (vsv[k] * winv);
+            const _Float16 hi = static_cast<_Float16>(w);
+            const _Float16 lo = static_cast<_Float16>(w - static_cast<float>(hi));
+            pb[k] = lo_row ? lo : hi;
+        }
+        lsum = lsum * alpha + ps;
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+            const int8_t* src = vt + vrow * D + (v_slot<D>(c, vrow) << 4) + 8 * h2;
+            const i32x2 vb = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(const_cast<int8_t*>(src)));
+            acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_f16(vb), pb, acc[c], 0, 0, 0);
+        }
+    };
+
+    // A finished segment of sequence b from registers (no LDS, no barrier):
+    // the output when it covers the whole sequence, else record gw + b.
+    auto emit_segment = [&](int b, bool complete) {
+        float lt = lsum;
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
+        const float fct = vref * (1.0f / kPScale);
+        const bool writer = r < G;
+        const size_t row = static_cast<size_t>(b) * a.Hq + hq0 + r;
+        const size_t rec = (static_cast<size_t>(gw) + b) * a.Hq + hq0 + r;
+        const float sc = complete ? fct / lt : fct;
+        const buf_rsrc recr = make_rsrc(a.part_acc + (static_cast<size_t>(gw) + b) * a.Hq * D, a.Hq * D * 4u);
+#pragma unroll
+        for (int c = 0; c < NB; c++) {
+            f32x4 o;
+            // Row r < G (hi part) adds row r + G (lo part): a DPP row shift left by G.
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                o[i] = (acc[c][i] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc[c][i]),
+                                                                                 0x100 + G, 0xF, 0xF, false))) * sc;
+            if (writer) {
+                if (complete) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) a.out[row * D + 16 * c + 4 * g + i] = o[i];
+                } else {
+                    // Device-coherent 16-byte store (sc1), as put_coherent.
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i_t, o), recr,
+                                                           ((hq0 + r) * D + 16 * c + 4 * g) * 4, 0, kCoherent);
+                }
+            }
+        }
+        if (!complete && writer && g == 0) {
+            put_coherent(a.part_ml + rec * 2, m);
+            put_coherent(a.part_ml + rec * 2 + 1, lt);
+        }
+    };
+    auto reset_state = [&]() {
+        m = -INFINITY;
+        lsum = 0.0f;
+        vref = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NB; c++) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+
+    // One wave's arrival for sequence b (lane 0; after the wave's record
+    // stores have completed): returns b when it completes the count of waves
+    // covering b, which then owns b's merge; the counter goes back to 0.
+    auto arrive = [&](int b) {
+        int done = -1;
+        if (lane == 0) {
+            const int bE = __builtin_amdgcn_readlane(e_l, b);
+            const int bn = __builtin_amdgcn_readlane(n_l, b);
+            const int cover = flat_wave_of(fs, bE + bn - 1) - flat_wave_of(fs, bE) + 1;
+            int* ctr = a.counters + static_cast<size_t>(b) * U + unit;
+            const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (prev + 1 == cover) {
+                __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next launch
+                done = b;
+            }
+        }
+        return __builtin_amdgcn_readfirstlane(__shfl(done, 0));
+    };
+
+    // Compute cursor (sequence of the tile being computed) and load cursor
+    // (sequence of the tile being loaded, one ahead); wave-uniform.
+    int pend = -1;       // this wave's partial first-segment record, not yet counted
+    int pend_merge = -1;  // a sequence this wave completed mid-range (merged at the end)
+    int cb = -1, cE = 0, cn = 0, clen = 0;
+    int from = tb;  // first tile of the current segment
+    const int ntiles = te - tb;
+    if (ntiles > 0) {
+        cb = seq_of(tb);
+        cE = __builtin_amdgcn_readlane(e_l, cb);
+        cn = __builtin_amdgcn_readlane(n_l, cb);
+        clen = __builtin_amdgcn_readlane(len_l, cb);
+        int lb = cb, lE = cE, ln = cn;  // load cursor
+        Tile ta, tb_;
+        set_load_seq(cb);
+        load_tile(ta, cb, (tb - cE) * kMTile, false);
+        load_q(cb);
+        if (app && tb == cE + cn - 1) load_new(cb);
+        prepare_q();
+        stage_v(ta, s_v[wv][0]);
+        // One iteration: tile it (in Tc, LDS buffer it & 1) is computed while
+        // tile it + 1 loads into Tn.
+        auto step = [&](Tile& Tc, Tile& Tn, int it) {
+            const int t = tb + it;
+            const bool more = it + 1 < ntiles;
+            // Tile t ends its sequence; the next tile starts the next non-empty one.
+            const bool switched = more && t + 1 == lE + ln;
+            if (switched) {
+                lb = seq_of(t + 1);
+                lE = __builtin_amdgcn_readlane(e_l, lb);
+                ln = __builtin_amdgcn_readlane(n_l, lb);
+                set_load_seq(lb);
+            }
+            load_tile(Tn, lb, (t + 1 - lE) * kMTile, !more);
+            if (switched) load_q(lb);
+            if (app && more && t + 1 == lE + ln - 1) load_new(lb);
+            int8_t* vt = s_v[wv][it & 1];
+            const int base = (t - cE) * kMTile;
+            if (app && t == cE + cn - 1) {
+                append_new(cb, clen - 1);
+                substitute_new(Tc, base, clen - 1, vt);
+            }
+            compute(Tc, base, clen, vt);
+            if (more && t == cE + cn - 1) {
+                // The segment ends inside the range: a middle segment is a
+                // whole sequence, the first one may be a sequence's tail.
+                const bool complete = from == cE;
+                emit_segment(cb, complete);
+                if (!complete) pend = cb;
+                cb = lb;
+                cE = lE;
+                cn = ln;
+                clen = __builtin_amdgcn_readlane(len_l, cb);
+                from = t + 1;
+                reset_state();
+                prepare_q();
+            }
+            if (more) stage_v(Tn, s_v[wv][(it + 1) & 1]);
+            if (pend >= 0) {
+                // Count the tail record now: the waits above have drained this
+                // wave's memory operations nearly (the record stores were
+                // issued before the next tile's last loads).
+                __builtin_amdgcn_s_waitcnt(0);
+                pend_merge = arrive(pend);
+                pend = -1;
+            }
+        };
+        int it = 0;
+        for (; it + 1 < ntiles; it += 2) {
+            step(ta, tb_, it);
+            step(tb_, ta, it + 1);
+        }
+        if (it < ntiles) step(ta, tb_, it);
+    }
+
+    // The last segment: output or record straight from registers, then its
+    // arrival (one wave), and the merge of any sequence whose count this wave
+    // completed (here, or mid-range for its first-segment tail).  No LDS and
+    // no barrier: waves finish independently.
+    if (ntiles == 0) return;
+    const bool last_done = from == cE && te == cE + cn;
+    emit_segment(cb, last_done);
+    int done1 = -1;
+    if (!last_done) {
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's record stores have completed
+        done1 = arrive(cb);
+    }
+    const int done0 = pend_merge;
+    if (done0 < 0 && done1 < 0) return;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int b = k == 0 ? done0 : done1;
+        if (b < 0) continue;
+        const int bE = __builtin_amdgcn_readlane(e_l, b);
+        const int bn = __builtin_amdgcn_readlane(n_l, b);
+        const int w0 = flat_wave_of(fs, bE);
+        const int w1 = flat_wave_of(fs, bE + bn - 1);
+        merge_wave_records<D, G>(a, b, w0, w1 - w0 + 1, hq0, lane);
+    }
+}
+
 }  // namespace
 
 int mfma_tile_tokens() { return kMBStep; }
@@ -530,7 +1150,13 @@ namespace {
 template <int D, int G>
 void launch_mfma_dg(const DecodeArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
     const bool paged = a.pages.table != nullptr;
-    if (a.fit_items > 0) {
+    if (a.flat) {
+        const bool app = a.k_new != nullptr;
+        if (paged && app) hipLaunchKernelGGL((decode_mfma_flat<D, G, true, true>), grid, block, 0, stream, a);
+        else if (paged) hipLaunchKernelGGL((decode_mfma_flat<D, G, true, false>), grid, block, 0, stream, a);
+        else if (app) hipLaunchKernelGGL((decode_mfma_flat<D, G, false, true>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((decode_mfma_flat<D, G, false, false>), grid, block, 0, stream, a);
+    } else if (a.fit_items > 0) {
         if (paged) hipLaunchKernelGGL((decode_mfma<D, G, true, true>), grid, block, 0, stream, a);
         else hipLaunchKernelGGL((decode_mfma<D, G, false, true>), grid, block, 0, stream, a);
     } else {

@@ -47,6 +47,8 @@ struct DecodeArgs {
     int sched_items;         // capacity of the schedule's item list
     int fit_items;           // > 0: the matrix-core kernel plans a ragged batch itself (locate_fit), this many items
     int fit_gran;            // chunk granularity of that plan (tokens)
+    int flat;                // matrix-core kernel, ragged batch: fit_items workgroups per work unit take
+                             // equal ranges of the sequences' tiles laid end to end (decode_mfma_flat)
     PageMap pages;           // paged layout, or pages.table == null (contiguous rows of cap tokens)
     int B, Hq, Hkv, G, cap, d;
     int uniform_len;         // used when lengths == null
@@ -77,6 +79,8 @@ constexpr int kSchedItemInts = 8;
 // Most sequences of a ragged batch the matrix-core kernel plans itself (one
 // per lane of a wave).
 constexpr int kFitMaxSeqs = 64;
+// Waves per workgroup of the matrix-core decode kernels.
+constexpr int kMfmaWaves = 4;
 
 // Which decode kernel a plan runs.
 enum class Kernel {
@@ -96,6 +100,7 @@ struct DecodePlan {
     bool counters;   // last-arriving split merges (fast path with a zeroed counter prefix)
     bool scheduled;  // ragged batch: the split schedule is computed on the device
     bool fit;        // ragged batch planned inside the matrix-core kernel (one round, no schedule launch)
+    bool flat;       // with fit: the flattened tile-stream plan (decode_mfma_flat)
     int sched_items;     // schedule item capacity (scheduled)
     int sched_target;    // workgroups the schedule aims for (scheduled)
     int sched_gran;      // chunk granularity in tokens (scheduled)
