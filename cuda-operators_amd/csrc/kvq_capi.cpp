@@ -178,18 +178,28 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
     const int U = Hkv * p.nsg;
     const bool fit_kernel = p.kernel == kvq::Kernel::Mfma || (p.kernel == kvq::Kernel::Valu && p.sg <= 2);
     const int fit_items = (p.kernel == kvq::Kernel::Mfma ? KVQ_FIT_TARGET_MFMA : KVQ_FIT_TARGET_VALU) / U;
+    // Flattened tile plan (decode_mfma_flat): the workgroups' waves take
+    // equal ranges of the sequences' tiles laid end to end.
+    // * A sequence covering w waves is merged from w records by one wave, so
+    //   batches averaging over 16 waves per sequence (4 * fit_items waves,
+    //   B < fit_items / 4) keep the per-sequence item plan below (two
+    //   sequences of 30-60K tokens: 53 us flat, 42 us itemised; B = 8,
+    //   4K-32K tokens: 57 / 56 us; B = 16, cfg2: 33.1 / 34.0 us).
+    // * Up to 64 sequences it replaces the one-round item plan or schedule
+    //   (B64 Hq32/Hkv8 L 1K-8K: 101 us flat, 143 us scheduled; with 8 heads
+    //   per kv head and append, L 512-4K: 69 / 83 us).
+    // * Beyond 64 the schedule's longest-first rounds balance long steps
+    //   better than one static split, whose waves' rate differences add up
+    //   (cfg4: 224 us flat, 205 us scheduled; B128 L 512-2K: 66 / 62 us), so
+    //   the flat plan keeps only small steps, at most 16 tiles per wave for
+    //   full-length sequences (B300 L 1-40: 26 / 34 us; B1000 L 0-256: 122 /
+    //   125 us).
+    // Record ids run to waves + B per query head.
+    const long flat_tiles = static_cast<long>(B) * ((max_len + kvq::kMfmaTile - 1) / kvq::kMfmaTile);
+    const bool flat_shape = B <= kvq::kFitMaxSeqs || flat_tiles <= 16L * kvq::kMfmaWaves * fit_items;
     if (ragged && requested == 0 && fused && p.kernel == kvq::Kernel::Mfma && fit_items >= 1 &&
-        B <= kvq::kFitMaxSeqs && 4 * B >= fit_items && static_cast<long>(B) * U <= kMaxCounters &&
+        B <= kvq::kFlatMaxSeqs && 4 * B >= fit_items && flat_shape && static_cast<long>(B) * U <= kMaxCounters &&
         max_len <= (1 << 30) && flat_enabled()) {
-        // Ragged batch of at most 64 sequences on the matrix cores: the
-        // workgroups' waves take equal ranges of the sequences' tiles laid end
-        // to end (decode_mfma_flat).  A sequence covering w waves is merged
-        // from w records by one wave, so batches with over 16 waves per
-        // sequence on average (4 * fit_items waves, B < fit_items / 4) keep
-        // the per-sequence item plan below (two sequences of 30-60K tokens:
-        // 53 us flat, 42 us itemised; B = 8, 4K-32K tokens: 57 / 56 us;
-        // B = 16, cfg2: 33.1 / 34.0 us).  Record ids run to waves + B per
-        // query head.
         p.fit = true;
         p.flat = true;
         p.counters = true;

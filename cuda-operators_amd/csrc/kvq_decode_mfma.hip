@@ -52,7 +52,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
 constexpr int kMWaves = kMfmaWaves;  // waves per workgroup
-constexpr int kMTile = 32;        // tokens per wave tile
+constexpr int kMTile = kMfmaTile;  // tokens per wave tile
 constexpr float kPScale = 32768.0f;  // PV weights are formed in [-2^15, 2^15] before the f16 split
 constexpr int kMBStep = kMTile * kMWaves;
 
@@ -638,6 +638,9 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     constexpr int NE = 2 * D / kWave;
     __shared__ __align__(16) int8_t s_v[kMWaves][2][kMTile * D];  // V tiles, per wave
     __shared__ __align__(16) int8_t s_newq[kMWaves][2][D];
+    __shared__ int s_E[kFlatMaxSeqs + 1];  // big batches: first tile of each sequence, then T
+    __shared__ int s_len[kFlatMaxSeqs];    // and its length
+    __shared__ int s_wsum[kMWaves];
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -654,32 +657,112 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     const int wv = __builtin_amdgcn_readfirstlane(wave);
     const int gw = item * kMWaves + wv;
 
-    // The plan: lane b holds sequence b's length, tiles and first tile.
+    // The plan.  A window of 64 sequences lives in lanes: lane j holds
+    // sequence wb0 + j's length, tiles and first tile.  Up to 64 sequences
+    // the window is the whole batch, scanned in lanes; beyond that the
+    // workgroup scans the lengths into LDS (first tiles and lengths of up to
+    // kFlatMaxSeqs sequences) and each wave's window starts at its first
+    // sequence, moving on when its range runs past 64 sequences.
     const int B = a.B;
-    const int len_l = lane < B ? seq_len_of(a, lane) : 0;
-    const int n_l = (len_l + kMTile - 1) / kMTile;
-    int incl = n_l;
+    int wb0 = 0, wcount = 0, wend = 0;  // window base, size, and the tile where it ends
+    int len_l = 0, n_l = 0, e_l = 0;
+    int T = 0;
+    const bool big = B > kWave;
+    if (!big) {
+        len_l = lane < B ? seq_len_of(a, lane) : 0;
+        n_l = (len_l + kMTile - 1) / kMTile;
+        int incl = n_l;
 #pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const int y = __shfl_up(incl, off);
-        if (lane >= off) incl += y;
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int y = __shfl_up(incl, off);
+            if (lane >= off) incl += y;
+        }
+        e_l = incl - n_l;
+        T = __builtin_amdgcn_readlane(incl, kWave - 1);
+        wcount = B;
+        wend = T;
+    } else {
+        // Thread t scans sequences [t * per, (t + 1) * per), then the block.
+        constexpr int kPer = kFlatMaxSeqs / (kMWaves * kWave);
+        const int per = (B + blockDim.x - 1) / blockDim.x;
+        const int s0 = threadIdx.x * per;
+        int lens[kPer];
+        int tot = 0;
+#pragma unroll
+        for (int k = 0; k < kPer; k++) {
+            lens[k] = (k < per && s0 + k < B) ? seq_len_of(a, s0 + k) : 0;
+            tot += (lens[k] + kMTile - 1) / kMTile;
+        }
+        int incl = tot;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int y = __shfl_up(incl, off);
+            if (lane >= off) incl += y;
+        }
+        if (lane == kWave - 1) s_wsum[wv] = incl;
+        __syncthreads();
+        int base = incl - tot;
+        for (int w = 0; w < wv; w++) base += s_wsum[w];
+        T = 0;
+#pragma unroll
+        for (int w = 0; w < kMWaves; w++) T += s_wsum[w];
+#pragma unroll
+        for (int k = 0; k < kPer; k++) {
+            if (k < per && s0 + k < B) {
+                s_E[s0 + k] = base;
+                s_len[s0 + k] = lens[k];
+                base += (lens[k] + kMTile - 1) / kMTile;
+            }
+        }
+        if (threadIdx.x == 0) s_E[B] = T;
+        __syncthreads();
     }
-    const int e_l = incl - n_l;
-    const int T = __builtin_amdgcn_readlane(incl, kWave - 1);
+    // Window at sequence b0 (big batches).
+    auto win_load = [&](int b0) {
+        wb0 = b0;
+        wcount = min(kWave, B - b0);
+        const bool in = lane < wcount;
+        e_l = in ? s_E[b0 + lane] : T;
+        n_l = in ? s_E[b0 + lane + 1] - e_l : 0;
+        len_l = in ? s_len[b0 + lane] : 0;
+        wend = s_E[b0 + wcount];
+    };
+    // The sequence holding tile t < T, by two rounds of 64-way search in LDS (big batches).
+    auto find_seq = [&](int t) {
+        const int step = (B + kWave - 1) / kWave;
+        const int i1 = min(B - 1, lane * step);
+        const int j1 = static_cast<int>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(s_E[i1] <= t &&
+                                                                                       lane * step < B))) - 1;
+        const int lo = j1 * step;
+        const int i2 = min(B - 1, lo + lane);
+        return lo + static_cast<int>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < step && s_E[i2] <= t &&
+                                                                                    lo + lane < B))) - 1;
+    };
     const FlatSplit fs = flat_split(T, Wn);
     const int tb = flat_start(fs, gw);
     const int te = flat_start(fs, gw + 1);
-    auto seq_of = [&](int t) {  // the sequence holding tile t < T
-        return static_cast<int>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < B && e_l <= t))) - 1;
+    if (big) win_load(tb < T ? find_seq(tb) : 0);
+    auto seq_of = [&](int t) {  // the sequence holding tile t < T; moves the window when t is past it
+        if (big && t >= wend) win_load(find_seq(t));
+        return wb0 + static_cast<int>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < wcount && e_l <= t))) -
+               1;
     };
+    // Plan entries of sequence b in the window.
+    auto plan_e = [&](int b) { return __builtin_amdgcn_readlane(e_l, b - wb0); };
+    auto plan_n = [&](int b) { return __builtin_amdgcn_readlane(n_l, b - wb0); };
+    auto plan_len = [&](int b) { return __builtin_amdgcn_readlane(len_l, b - wb0); };
 
     // Zero rows of empty sequences, once per work unit.
     if (item == 0 && wv == 0) {
-        unsigned long long empty = __builtin_amdgcn_ballot_w64(lane < B && len_l == 0);
-        while (empty) {
-            const int b = __builtin_ctzll(empty);
-            empty &= empty - 1;
-            for (int i = lane; i < G * D; i += kWave) a.out[(static_cast<size_t>(b) * a.Hq + hq0) * D + i] = 0.0f;
+        for (int c0 = 0; c0 < B; c0 += kWave) {
+            const int b = c0 + lane;
+            const int len = b < B ? (big ? s_len[b] : len_l) : 1;
+            unsigned long long empty = __builtin_amdgcn_ballot_w64(len == 0);
+            while (empty) {
+                const int be = c0 + __builtin_ctzll(empty);
+                empty &= empty - 1;
+                for (int i = lane; i < G * D; i += kWave) a.out[(static_cast<size_t>(be) * a.Hq + hq0) * D + i] = 0.0f;
+            }
         }
     }
 
@@ -1018,11 +1101,9 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // One wave's arrival for sequence b (lane 0; after the wave's record
     // stores have completed): returns b when it completes the count of waves
     // covering b, which then owns b's merge; the counter goes back to 0.
-    auto arrive = [&](int b) {
+    auto arrive = [&](int b, int bE, int bn) {
         int done = -1;
         if (lane == 0) {
-            const int bE = __builtin_amdgcn_readlane(e_l, b);
-            const int bn = __builtin_amdgcn_readlane(n_l, b);
             const int cover = flat_wave_of(fs, bE + bn - 1) - flat_wave_of(fs, bE) + 1;
             int* ctr = a.counters + static_cast<size_t>(b) * U + unit;
             const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1036,16 +1117,16 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
 
     // Compute cursor (sequence of the tile being computed) and load cursor
     // (sequence of the tile being loaded, one ahead); wave-uniform.
-    int pend = -1;       // this wave's partial first-segment record, not yet counted
-    int pend_merge = -1;  // a sequence this wave completed mid-range (merged at the end)
+    int pend = -1, pend_e = 0, pend_n = 0;  // this wave's partial first-segment record, not yet counted
+    int pm = -1, pm_e = 0, pm_n = 0;        // a sequence this wave completed mid-range (merged at the end)
     int cb = -1, cE = 0, cn = 0, clen = 0;
     int from = tb;  // first tile of the current segment
     const int ntiles = te - tb;
     if (ntiles > 0) {
         cb = seq_of(tb);
-        cE = __builtin_amdgcn_readlane(e_l, cb);
-        cn = __builtin_amdgcn_readlane(n_l, cb);
-        clen = __builtin_amdgcn_readlane(len_l, cb);
+        cE = plan_e(cb);
+        cn = plan_n(cb);
+        clen = plan_len(cb);
         int lb = cb, lE = cE, ln = cn;  // load cursor
         Tile ta, tb_;
         set_load_seq(cb);
@@ -1063,8 +1144,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             const bool switched = more && t + 1 == lE + ln;
             if (switched) {
                 lb = seq_of(t + 1);
-                lE = __builtin_amdgcn_readlane(e_l, lb);
-                ln = __builtin_amdgcn_readlane(n_l, lb);
+                lE = plan_e(lb);
+                ln = plan_n(lb);
                 set_load_seq(lb);
             }
             load_tile(Tn, lb, (t + 1 - lE) * kMTile, !more);
@@ -1082,11 +1163,11 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
                 // whole sequence, the first one may be a sequence's tail.
                 const bool complete = from == cE;
                 emit_segment(cb, complete);
-                if (!complete) pend = cb;
+                if (!complete) pend = cb, pend_e = cE, pend_n = cn;
                 cb = lb;
                 cE = lE;
                 cn = ln;
-                clen = __builtin_amdgcn_readlane(len_l, cb);
+                clen = plan_len(cb);
                 from = t + 1;
                 reset_state();
                 prepare_q();
@@ -1097,7 +1178,9 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
                 // wave's memory operations nearly (the record stores were
                 // issued before the next tile's last loads).
                 __builtin_amdgcn_s_waitcnt(0);
-                pend_merge = arrive(pend);
+                pm = arrive(pend, pend_e, pend_n);
+                pm_e = pend_e;
+                pm_n = pend_n;
                 pend = -1;
             }
         };
@@ -1119,16 +1202,15 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     int done1 = -1;
     if (!last_done) {
         __builtin_amdgcn_s_waitcnt(0);  // this wave's record stores have completed
-        done1 = arrive(cb);
+        done1 = arrive(cb, cE, cn);
     }
-    const int done0 = pend_merge;
-    if (done0 < 0 && done1 < 0) return;
+    if (pm < 0 && done1 < 0) return;
 #pragma unroll
     for (int k = 0; k < 2; k++) {
-        const int b = k == 0 ? done0 : done1;
+        const int b = k == 0 ? pm : done1;
         if (b < 0) continue;
-        const int bE = __builtin_amdgcn_readlane(e_l, b);
-        const int bn = __builtin_amdgcn_readlane(n_l, b);
+        const int bE = k == 0 ? pm_e : cE;
+        const int bn = k == 0 ? pm_n : cn;
         const int w0 = flat_wave_of(fs, bE);
         const int w1 = flat_wave_of(fs, bE + bn - 1);
         merge_wave_records<D, G>(a, b, w0, w1 - w0 + 1, hq0, lane);

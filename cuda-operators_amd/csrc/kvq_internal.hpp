@@ -79,8 +79,12 @@ constexpr int kSchedItemInts = 8;
 // Most sequences of a ragged batch the matrix-core kernel plans itself (one
 // per lane of a wave).
 constexpr int kFitMaxSeqs = 64;
-// Waves per workgroup of the matrix-core decode kernels.
+// Waves per workgroup of the matrix-core decode kernels, and tokens per wave tile.
 constexpr int kMfmaWaves = 4;
+constexpr int kMfmaTile = 32;
+// Most sequences of a ragged batch under the flattened tile plan of the
+// matrix-core kernel (their first tiles and lengths are scanned into LDS).
+constexpr int kFlatMaxSeqs = 4096;
 
 // Which decode kernel a plan runs.
 enum class Kernel {

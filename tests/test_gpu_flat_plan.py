@@ -180,3 +180,35 @@ def test_repeated_launches_new_lengths(o):
         dec()
         torch.cuda.synchronize()
         assert np.array_equal(_bits(down(out)), _bits(first)), f"launch {it} not repeatable"
+
+
+@pytest.mark.parametrize("B,cap", [(65, 256), (256, 64), (1000, 64)])
+def test_big_batch_plan(o, B, cap):
+    """More than 64 sequences in a small step (at most 16 tiles per wave):
+    lengths scanned into LDS, each wave's window of 64 sequences starting at
+    its first one (cfg4's head layout at short lengths, with the fused append
+    and empty sequences)."""
+    rng = np.random.default_rng(B)
+    Hkv, G, d = 8, 8, 128
+    lengths = rng.integers(0, cap + 1, B).astype(np.int32)
+    lengths[:5] = [0, 1, 32, 33, cap]
+    _check(o, B, Hkv, G, cap, d, lengths, rng, append=True, dist="student_t", what=f"B={B}")
+
+
+def test_window_moves_along_the_range(o):
+    """1500 sequences of 0-32 tokens with a run of 300 empty ones: the wave
+    whose range crosses the run spans more than 64 sequences, so its window
+    moves on."""
+    rng = np.random.default_rng(2000)
+    B, Hkv, G, cap, d = 1500, 8, 4, 32, 64
+    lengths = rng.integers(0, cap + 1, B).astype(np.int32)
+    lengths[100:400] = 0  # a run of empty sequences longer than a window
+    _check(o, B, Hkv, G, cap, d, lengths, rng, append=True, what="window")
+
+
+def test_max_batch_plan(o):
+    """kFlatMaxSeqs = 4096 sequences of 1-5 tokens."""
+    rng = np.random.default_rng(4096)
+    B, Hkv, G, cap, d = 4096, 1, 4, 8, 64
+    lengths = rng.integers(1, 6, B).astype(np.int32)
+    _check(o, B, Hkv, G, cap, d, lengths, rng, what="4096")
