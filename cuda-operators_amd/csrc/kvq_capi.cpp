@@ -195,7 +195,7 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
     //   full-length sequences (B300 L 1-40: 26 / 34 us; B1000 L 0-256: 122 /
     //   125 us).
     // Record ids run to waves + B per query head.
-    const long flat_tiles = static_cast<long>(B) * ((max_len + kvq::kMfmaTile - 1) / kvq::kMfmaTile);
+    const long flat_tiles = static_cast<long>(B) * ((static_cast<long>(max_len) + kvq::kMfmaTile - 1) / kvq::kMfmaTile);
     const bool flat_shape = B <= kvq::kFitMaxSeqs || flat_tiles <= 16L * kvq::kMfmaWaves * fit_items;
     if (ragged && requested == 0 && fused && p.kernel == kvq::Kernel::Mfma && fit_items >= 1 &&
         B <= kvq::kFlatMaxSeqs && 4 * B >= fit_items && flat_shape && static_cast<long>(B) * U <= kMaxCounters &&
@@ -269,13 +269,13 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
             splits = std::max<long>(1, kTargetWorkgroupsMfma / units);
         else
             splits = (kTargetWorkgroupsValu + units - 1) / units;
-        splits = std::min<long>(splits, (max_len + gran - 1) / gran);
+        splits = std::min<long>(splits, (static_cast<long>(max_len) + gran - 1) / gran);
         splits = std::max<long>(1, std::min<long>(splits, std::max(max_splits, 1)));
         chunk = static_cast<int>((max_len + splits - 1) / splits);
         if (splits > 1) chunk = static_cast<int>(round_up(static_cast<size_t>(chunk), gran));
     }
     p.chunk = chunk;
-    p.splits = (max_len + chunk - 1) / chunk;
+    p.splits = static_cast<int>((static_cast<long>(max_len) + chunk - 1) / chunk);
     if (p.splits > 1) {
         const size_t recs = static_cast<size_t>(B) * Hq * p.splits;
         // A workspace in fused layout always reserves the counter prefix, even

@@ -44,6 +44,7 @@
  * Build: see oracle/Makefile (gcc -O3 -fopenmp -ffp-contract=off, no -ffast-math).
  */
 #include <float.h>
+#include <limits.h>
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -68,6 +69,10 @@
 #define PLANT_NO_VSCALE 9   /* value dequant drops v_scale                  */
 #define PLANT_ATT_INV_D 10  /* dense attention: 1/d instead of 1/sqrt(d)     */
 #define PLANT_ATT_V_T 11    /* dense attention: V indexed [d][n]             */
+/* Memory and undefined-behaviour faults, built only by the sanitizer target
+ * (oracle/Makefile `sanitize`) to show that a sanitizer report fails the run: */
+#define PLANT_OOB_READ 12   /* softmax loop runs one past the score scratch */
+#define PLANT_INT_OVF 13    /* signed int overflow                          */
 
 int kvq_ref_plant_id(void) { return PLANT; }
 
@@ -107,7 +112,11 @@ static void head_f32(const float* q, const int8_t* k, const int8_t* v,
         max_score = fmaxf(max_score, score);
     }
     float denom = 0.0f;
+#if PLANT == PLANT_OOB_READ
+    for (int t = 0; t <= n; t++) {
+#else
     for (int t = 0; t < n; t++) {
+#endif
 #if PLANT == PLANT_EXP_SIGN
         scores[t] = expf(max_score - scores[t]);
 #else
@@ -161,6 +170,11 @@ void kvq_ref_head_f32(const float* Q, const int8_t* K, const int8_t* V,
                       const float* ks, const float* vs, float* out,
                       int num_heads, int seq_len, int head_dim) {
     float* scores = (float*)malloc(sizeof(float) * (size_t)seq_len);
+#if PLANT == PLANT_INT_OVF
+    volatile int big = INT_MAX;
+    const int wrapped = big + num_heads;
+    if (wrapped == 0) num_heads = 0;
+#endif
     for (int h = 0; h < num_heads; h++) {
         const size_t kv = (size_t)h * seq_len * head_dim;
         head_f32(Q + (size_t)h * head_dim, K + kv, V + kv, ks + (size_t)h * seq_len,

@@ -20,7 +20,12 @@ import threading
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# KVQ_ORACLE_SANITIZED=1 selects the AddressSanitizer + UBSan builds
+# (oracle/_asan, make target `sanitize`); the process must then run with the
+# ASan runtime preloaded (tests/test_sanitizers_cpu.py does this).
+SANITIZED = os.environ.get("KVQ_ORACLE_SANITIZED", "") == "1"
+LIB_DIR = os.path.join(HERE, "_asan") if SANITIZED else HERE
+LIB_PATH = os.path.join(LIB_DIR, "liboracle.so")
 
 _c_f32p = ctypes.POINTER(ctypes.c_float)
 _c_f64p = ctypes.POINTER(ctypes.c_double)
@@ -33,12 +38,12 @@ _libs: dict[str, ctypes.CDLL] = {}
 
 def build(plants: bool = False) -> None:
     """Compile the oracle (and optionally the planted-mistake variants) with make."""
-    targets = ["all"] + (["plants"] if plants else [])
+    targets = ["sanitize"] if SANITIZED else ["all"] + (["plants"] if plants else [])
     subprocess.run(["make", "-s", "-C", HERE] + targets, check=True)
 
 
 def plant_path(plant: int) -> str:
-    return os.path.join(HERE, "_plant", f"liboracle_plant{plant}.so")
+    return os.path.join(LIB_DIR, "_plant", f"liboracle_plant{plant}.so")
 
 
 def _load(path: str) -> ctypes.CDLL:

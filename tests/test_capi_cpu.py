@@ -145,30 +145,34 @@ def _ru(x, a=256):
     return (x + a - 1) // a * a
 
 
-@pytest.mark.parametrize("B", [8, 24, 31, 32, 64, 65, 1025])
+@pytest.mark.parametrize("B", [8, 24, 31, 32, 64, 65, 512, 513, 1025])
 def test_matrix_core_plan_by_workspace(L, B):
     """Grouped-query heads at d = 128 (matrix-core kernel, 4 heads per
-    workgroup, U = Hkv work units per sequence), ragged lengths: up to 64
-    sequences the kernel plans the batch itself with S = 256 / U workgroups
-    per work unit -- the flattened tile plan (records for 4 S waves + B ids)
-    when B >= S / 4, otherwise whole items per sequence (S items of
-    records); beyond 64 sequences the device split schedule's words come on
-    top of its own B + 512 / U + 1 items of records.  Records hold (d + 2)
-    floats per query head after the counter block."""
-    Hq, Hkv, d = 8, 2, 128
-    p = _params(batch=B, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=d, lengths=FAKE, capacity=512,
-                max_seq_len=512)
+    workgroup, U = Hkv work units per sequence), ragged lengths: the kernel
+    plans the batch itself with S = 256 / U workgroups per work unit -- the
+    flattened tile plan (records for 4 S waves + B ids) when B >= S / 4 and
+    either B <= 64 or the batch has at most 16 tiles of 32 tokens per wave at
+    full length; below S / 4 sequences whole items per sequence (S items of
+    records); otherwise the device split schedule, whose words come on top of
+    its own B + 512 / U + 1 items of records.  Records hold (d + 2) floats
+    per query head after the counter block."""
+    Hq, Hkv, d, cap = 8, 2, 128, 512
+    p = _params(batch=B, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=d, lengths=FAKE, capacity=cap,
+                max_seq_len=cap)
     n = L.kvq_decode_workspace_size(ctypes.byref(p))
     info = kvq.decode_plan(p)
     S = 256 // Hkv
-    if B <= 64:
+    flat = 4 * B >= S and (B <= 64 or B * (cap // 32) <= 16 * 4 * S)
+    if flat or B <= 64:
         assert info.split_plan == kvq.SPLITS_IN_KERNEL
-        items = 4 * S + B if 4 * B >= S else S
+        items = 4 * S + B if flat else S
         assert n == 256 * 1024 + _ru(items * Hq * 2 * 4) + _ru(items * Hq * d * 4)
     else:
+        assert info.split_plan == kvq.SPLITS_SCHEDULE
         items = B + (512 + Hkv - 1) // Hkv + 1
         sched = _ru((4 + 8 * items + 2 * B) * 4)
         assert n == 256 * 1024 + sched + _ru(items * Hq * 2 * 4) + _ru(items * Hq * d * 4)
+    assert (B in (512, 65)) == (flat and B > 64)
 
 
 def test_append_and_quantize_reject_before_hip(L):
