@@ -194,7 +194,9 @@ def provenance(torch, kvq):
             rocm = f.read().strip()
     except OSError:
         pass
-    hipcc = cmd("/opt/rocm/bin/hipcc", "--version")
+    # The compiler version comes from the build record: running hipcc here
+    # would start further programs under a profiler's preload.
+    hipcc = (build_info or {}).get("hipcc")
     props = torch.cuda.get_device_properties(0)
     return {
         "git_sha": cmd("git", "-C", REPO, "rev-parse", "HEAD"),
@@ -204,7 +206,7 @@ def provenance(torch, kvq):
         "bench_sha256": _sha256_files([os.path.abspath(__file__)]),
         "library": kvq.version(),
         "rocm": rocm,
-        "hipcc": hipcc.splitlines()[0] if hipcc else None,
+        "hipcc": hipcc,
         "torch": torch.__version__,
         "gpu": props.name,
         "gpu_arch": getattr(props, "gcnArchName", None),
