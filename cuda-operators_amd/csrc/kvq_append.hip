@@ -99,17 +99,60 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const Pre
     float* so = kv ? a.vs : a.ks;
     constexpr int ESZ = BF16 ? 2 : 4;
     const unsigned step = gridDim.x * kPrefillWaves * RPW * kPrefillU;
+    const buf_rsrc srs = make_rsrc(a.start, a.start ? static_cast<unsigned>(a.nseq) * 4u : 0u);
+    const int start0 = a.start ? 0 : a.uniform_start;
+    const bool paged = a.pages.table != nullptr;
+    const size_t tbytes = paged ? static_cast<size_t>(a.nseq) * a.pages.max_pages * 4 : 0;
+    const buf_rsrc trs = make_rsrc(a.pages.table, static_cast<unsigned>(min(tbytes, static_cast<size_t>(0x7fffffff))));
     for (unsigned r0 = (blockIdx.x * kPrefillWaves + wave) * RPW * kPrefillU; r0 < a.rows; r0 += step) {
+        // The kPrefillU row loads go out together and unconditionally (a row
+        // past the end rereads the last row and is dropped below), so no
+        // load waits for another.
         int4 raw[kPrefillU];
+        unsigned row[kPrefillU];
 #pragma unroll
         for (int u = 0; u < kPrefillU; u++) {
-            const unsigned row = r0 + u * RPW + slot;
-            raw[u] = row < a.rows ? *reinterpret_cast<const int4*>(x + (static_cast<size_t>(row) * D + ls * EPL) * ESZ)
-                                  : make_int4(0, 0, 0, 0);
+            row[u] = r0 + u * RPW + slot;
+            const unsigned rc = min(row[u], a.rows - 1);
+            raw[u] = *reinterpret_cast<const int4*>(x + (static_cast<size_t>(rc) * D + ls * EPL) * ESZ);
+        }
+        // Each row's destination: (b, kv head, token) from the row index,
+        // then the cache row.  start[b] and the page-table entries come
+        // through buffer resources (a null start, or an index outside the
+        // table, reads 0), so the loads of all kPrefillU rows are
+        // unconditional and in flight together.  -1: the row is skipped.
+        int pos[kPrefillU], bb[kPrefillU], hh[kPrefillU];
+#pragma unroll
+        for (int u = 0; u < kPrefillU; u++) {
+            const unsigned rc = min(row[u], a.rows - 1);
+            const unsigned bh = fastdiv(rc, a.divL);
+            bb[u] = static_cast<int>(fastdiv(bh, a.divH));
+            hh[u] = static_cast<int>(bh - static_cast<unsigned>(bb[u]) * a.Hkv);
+            pos[u] = static_cast<int>(rc - bh * a.L) + start0 + buffer_load4(srs, bb[u] * 4, 0);
+        }
+        long long orow[kPrefillU];
+        if (paged) {
+            int page[kPrefillU], pi[kPrefillU];
+#pragma unroll
+            for (int u = 0; u < kPrefillU; u++) {
+                pi[u] = a.pages.shift >= 0 ? pos[u] >> a.pages.shift : pos[u] / a.pages.size;
+                page[u] = buffer_load4(trs, (bb[u] * a.pages.max_pages + pi[u]) * 4, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < kPrefillU; u++) {
+                const int pg = min(max(page[u], 0), a.pages.num_pages - 1);
+                orow[u] = (static_cast<long long>(pg) * a.Hkv + hh[u]) * a.pages.size + (pos[u] - pi[u] * a.pages.size);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < kPrefillU; u++)
+                orow[u] = (static_cast<long long>(bb[u]) * a.Hkv + hh[u]) * a.cap + pos[u];
         }
 #pragma unroll
+        for (int u = 0; u < kPrefillU; u++)
+            if (!(row[u] < a.rows && pos[u] >= 0 && pos[u] < a.cap)) orow[u] = -1;
+#pragma unroll
         for (int u = 0; u < kPrefillU; u++) {
-            const unsigned row = r0 + u * RPW + slot;
             float e[EPL];
             const int w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
 #pragma unroll
@@ -122,24 +165,17 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const Pre
 #pragma unroll
             for (int i = 0; i < EPL; i++) am = fmaxf(am, fabsf(e[i]));
             const float scale = quant_scale(lanes_max<LPR>(am));
-            if (row >= a.rows) continue;
-            const unsigned bh = fastdiv(row, a.divL);
-            const int t = static_cast<int>(row - bh * a.L);
-            const int b = static_cast<int>(fastdiv(bh, a.divH));
-            const int h = static_cast<int>(bh - static_cast<unsigned>(b) * a.Hkv);
-            const int pos = (a.start ? a.start[b] : a.uniform_start) + t;
-            if (pos < 0 || pos >= a.cap) continue;
-            const size_t orow = cache_row(a.pages, a.Hkv, a.cap, b, h, pos);
+            if (orow[u] < 0) continue;
+            const size_t o = static_cast<size_t>(orow[u]);
             int qv[EPL];
-#pragma unroll
-            for (int i = 0; i < EPL; i++) qv[i] = quant_one(e[i], scale);
+            quant_row<EPL>(e, scale, qv);
             if constexpr (BF16) {
                 const int2 pk = make_int2(pack4(qv[0], qv[1], qv[2], qv[3]), pack4(qv[4], qv[5], qv[6], qv[7]));
-                *reinterpret_cast<int2*>(qo + orow * D + ls * EPL) = pk;
+                *reinterpret_cast<int2*>(qo + o * D + ls * EPL) = pk;
             } else {
-                *reinterpret_cast<int*>(qo + orow * D + ls * EPL) = pack4(qv[0], qv[1], qv[2], qv[3]);
+                *reinterpret_cast<int*>(qo + o * D + ls * EPL) = pack4(qv[0], qv[1], qv[2], qv[3]);
             }
-            if (ls == 0) so[orow] = scale;
+            if (ls == 0) so[o] = scale;
         }
     }
 }

@@ -800,6 +800,7 @@ hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, 
         a.cap = static_cast<int>(rows);
         a.rows = static_cast<unsigned>(rows);
         a.planes = 1;
+        a.nseq = 1;
         a.pages = kvq::PageMap{nullptr, 0, 0, 0, -1};
         return finish_call(kvq::launch_prefill(a, head_dim, false, true, stream), stream);
     }
@@ -891,6 +892,7 @@ hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t 
     a.vs = p->v_scale;
     a.start = p->start;
     a.uniform_start = p->uniform_start;
+    a.nseq = p->batch;
     a.Hkv = p->num_kv_heads;
     a.L = p->tokens;
     a.divL = kvq::make_fastdiv(static_cast<uint32_t>(std::max(p->tokens, 1)));

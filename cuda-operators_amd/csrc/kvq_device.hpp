@@ -136,6 +136,45 @@ __device__ __forceinline__ int quant_one(float x, float scale) {
     return static_cast<int>(y);
 }
 
+// The same quantisation of N elements of one row, with the quotient taken as
+// x * rcp(scale) instead of the IEEE divide (a standard division by a
+// reciprocal with an error-bounded exactness test; e.g. Muller et al.,
+// Handbook of Floating-Point Arithmetic, 2nd ed., sec. 4.9 / 5.3).  The result
+// is bit-identical to quant_one for every input:
+// * |x| <= amax and scale = RN(amax / 127), so |x / scale| < 128.
+// * v_rcp_f32 is within 1 ulp (relative 2^-23) of 1 / scale and the product
+//   rounds once (2^-24), so the fast quotient q is within 1.5 * 2^-23 * 128 =
+//   1.5 * 2^-16 of x / scale; the IEEE quotient Q is within 2^-24 * 128 =
+//   2^-17 of it; hence |q - Q| <= 2^-15.
+// * rintf changes value only at half-integers, so rintf(q) == rintf(Q)
+//   whenever q is more than 2^-15 from every half-integer (then Q lies on
+//   the same side and is not itself a tie).  The test also holds when the
+//   compiler fuses y - n into fma(x, rinv, -n): then it measures the exact
+//   product P, with |P - Q| <= 1.5 * 2^-16 and |y - P| <= 2^-17, both below
+//   the margin, so q, P and Q round alike.  Lanes with an element within
+//   2^-15 of one (about one element in 16000), or with a scale outside
+//   [2^-100, 2^100] (zero, subnormal or non-finite scales included), redo the
+//   row part with quant_one.
+// Cost per element: multiply, rint, subtract, compare, clamp, convert --
+// against the IEEE divide's ten instructions.
+template <int N>
+__device__ __forceinline__ void quant_row(const float (&x)[N], float scale, int (&q)[N]) {
+    const bool normal = scale >= 0x1p-100f && scale <= 0x1p100f;
+    const float rinv = __builtin_amdgcn_rcpf(normal ? scale : 1.0f);
+    float dmax = 0.0f;  // largest |y - rint(y)| of the lane's elements
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const float y = x[i] * rinv;
+        const float n = __builtin_rintf(y);
+        dmax = fmaxf(dmax, fabsf(y - n));
+        q[i] = static_cast<int>(fminf(fmaxf(n, -127.0f), 127.0f));
+    }
+    if (!normal || dmax >= 0.5f - 0x1p-15f) {
+#pragma unroll
+        for (int i = 0; i < N; i++) q[i] = quant_one(x[i], scale);
+    }
+}
+
 __device__ __forceinline__ int pack4(int a, int b, int c, int d) {
     return (a & 0xff) | ((b & 0xff) << 8) | ((c & 0xff) << 16) | (static_cast<int>(static_cast<unsigned>(d & 0xff) << 24));
 }

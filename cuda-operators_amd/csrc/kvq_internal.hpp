@@ -146,6 +146,7 @@ struct PrefillArgs {
     FastDiv divL, divH;  // division of row indices by L and Hkv
     unsigned rows;
     int planes;  // 2: K and V; 1: K only
+    int nseq;    // sequences (entries of start, rows of the page table)
     PageMap pages;
 };
 // vec_ok: 16-byte aligned inputs and 8-byte aligned caches (tuned kernel for

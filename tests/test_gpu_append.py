@@ -116,6 +116,48 @@ def test_quantize_near_ties_bit_exact(d):
     assert np.array_equal(down(k)[0, 0], bq) and np.array_equal(_bits(down(ks)[0, 0]), _bits(bs))
 
 
+def threshold_rows(rng, d, rows):
+    """Rows whose quotients x / scale sit near half-integers at distances
+    around 2^-15, where the prefill quantiser switches from its reciprocal
+    product to the IEEE quotient: delta in {2^-17, 2^-16, 2^-15 * (1 +- 1/8),
+    2^-14, 2^-12} either side of k + 1/2, for k across the int8 range."""
+    deltas = np.array([2.0 ** -17, 2.0 ** -16, 2.0 ** -15 * 0.875, 2.0 ** -15, 2.0 ** -15 * 1.125,
+                       2.0 ** -14, 2.0 ** -12])
+    out = np.empty((rows, d), np.float32)
+    for r in range(rows):
+        amax = np.float32(np.exp(rng.uniform(-20.0, 20.0)))
+        scale = np.float64(np.float32(amax / np.float32(127.0)))
+        k = rng.integers(-127, 127, d - 1).astype(np.float64)
+        sgn = rng.choice([-1.0, 1.0], d - 1)
+        dl = rng.choice(deltas, d - 1)
+        x = np.clip(((k + 0.5 + sgn * dl) * scale).astype(np.float32), -amax, amax)
+        out[r, 0] = amax if r % 2 == 0 else -amax
+        out[r, 1:] = x
+    return out
+
+
+@pytest.mark.parametrize("d", [32, 128, 256])
+def test_quantize_fast_path_threshold(d):
+    """Bit-exact on both sides of the reciprocal path's exactness test, fp32
+    and bf16 inputs."""
+    o = orc.get()
+    rng = np.random.default_rng(300 + d)
+    x = threshold_rows(rng, d, 1024)
+    gq, gs = kvq.quantize_rows(up(x))
+    torch.cuda.synchronize()
+    wq, ws = o.quantize_rows(x)
+    assert np.array_equal(_bits(down(gs)), _bits(ws))
+    diff = np.argwhere(down(gq) != wq)
+    assert diff.size == 0, f"{len(diff)} elements differ, first {diff[:5].tolist()}"
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    k = torch.zeros((1, 1, x.shape[0], d), dtype=torch.int8, device="cuda")
+    ks = torch.zeros((1, 1, x.shape[0]), dtype=torch.float32, device="cuda")
+    kvq.prefill(xb.view(1, 1, -1, d).cuda(), xb.view(1, 1, -1, d).cuda(), k, k.clone(), ks, ks.clone())
+    torch.cuda.synchronize()
+    bq, bs = o.quantize_rows(xb.to(torch.float32).numpy())
+    assert np.array_equal(down(k)[0, 0], bq) and np.array_equal(_bits(down(ks)[0, 0]), _bits(bs))
+
+
 def test_quantize_many_rows():
     """A bulk prefill-sized tensor (grid-stride path) stays bit-exact."""
     o = orc.get()
