@@ -517,7 +517,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
 
 
 // ---------------------------------------------------------------------------
-// decode_mfma_flat: a ragged batch of at most kFitMaxSeqs sequences, balanced
+// decode_mfma_flat: a ragged batch of at most kFlatMaxSeqs sequences, balanced
 // over waves rather than over whole work items.
 //
 // For one work unit (kv head, head group) the sequences' 32-token tiles are
@@ -527,21 +527,21 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
 // one), whatever the lengths, where a plan of whole items per sequence waits
 // for its largest item (cfg2: 1.26-1.36x the mean).  A wave's range may cross
 // sequence boundaries: the tile loads run one tile ahead across the switch
-// (the next sequence's q limbs are loaded with its first tile), so a switch
-// costs no pipeline drain.  Per wave:
-// * a middle segment (a whole sequence) writes its output directly;
-// * a first segment that ends inside the range (the tail of a sequence begun
-//   by earlier waves) writes a partial record with record id gw + b;
-// * the last segment stays in registers.  At the end the workgroup's waves
-//   whose last segments share a sequence (a run of consecutive waves) combine
-//   through LDS into one output or one record (id of the run's first wave + b).
-// Record ids gw + b are distinct for distinct (wave, sequence) pairs because
-// both grow along the stream.  Arrivals are counted in waves: a record adds
-// the number of waves it stands for, and the arrival that completes the count
-// of waves covering b (known from the plan) merges b's records: one per
-// workgroup whose waves end in b, plus the tail record of the wave in which b
-// ends, all located from the plan (merge_runs).  Every wave computes the same
-// plan from the device lengths with lane operations (lane b holds sequence b).
+// (the next sequence's q is loaded with its first tile), so a switch costs no
+// pipeline drain.  Per wave, straight from registers (no LDS, no barrier):
+// * a segment that covers a whole sequence writes its output;
+// * any other segment writes a partial record with id gw + b (gw: the
+//   wave's index in the unit).  Ids gw + b are distinct for distinct (wave,
+//   sequence) pairs because both grow along the stream.
+// Each record counts one arrival on its sequence's counter; the arrival that
+// completes the count of waves covering b (known from the plan) merges b's
+// records (merge_wave_records, one wave) and resets the counter.  A wave's
+// first segment, when it is a sequence's tail, arrives as soon as its stores
+// have drained, inside the tile loop, so that merge overlaps other waves'
+// streaming.  Every wave computes the same plan from the device lengths:
+// with lane operations up to 64 sequences (lane b holds sequence b), and
+// beyond that from a block-wide scan of the lengths into LDS, through a
+// window of 64 sequences that moves along the wave's range.
 // ---------------------------------------------------------------------------
 
 // A stream of T tiles over W waves: with q = T / W and r = T % W, wave j
