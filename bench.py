@@ -252,6 +252,8 @@ def kernel_name(kvq, dec):
         return "paged"
     info = kvq.decode_plan(dec.params)
     name = f"{names[info.kernel]}<{dec.params.head_dim},{info.heads_per_group}>"
+    if info.split_plan == kvq.SPLITS_TILES:
+        return f"decode_mfma_flat<{dec.params.head_dim},{info.heads_per_group}> (tile-stream plan in-kernel)"
     if info.split_plan == kvq.SPLITS_IN_KERNEL:
         return name + " (split plan in-kernel)"
     if info.split_plan == kvq.SPLITS_SCHEDULE:

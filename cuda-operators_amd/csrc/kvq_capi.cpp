@@ -407,7 +407,10 @@ kvq_plan_info decode_info(const DecodePlan& p) {
                : p.kernel == kvq::Kernel::Valu ? KVQ_KERNEL_DECODE_VALU
                                                : KVQ_KERNEL_DECODE_GENERIC;
     r.heads_per_group = p.sg;
-    r.split_plan = p.fit ? KVQ_SPLITS_IN_KERNEL : p.scheduled ? KVQ_SPLITS_SCHEDULE : KVQ_SPLITS_STATIC;
+    r.split_plan = p.flat        ? KVQ_SPLITS_TILES
+                   : p.fit       ? KVQ_SPLITS_IN_KERNEL
+                   : p.scheduled ? KVQ_SPLITS_SCHEDULE
+                                 : KVQ_SPLITS_STATIC;
     r.splits = r.split_plan == KVQ_SPLITS_STATIC ? p.splits : 0;
     r.chunk = r.split_plan == KVQ_SPLITS_STATIC ? p.chunk : 0;
     r.query_block = 0;

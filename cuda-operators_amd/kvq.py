@@ -111,7 +111,7 @@ class PlanInfo(ctypes.Structure):
 
 KERNEL_DECODE_GENERIC, KERNEL_DECODE_VALU, KERNEL_DECODE_MFMA = 0, 1, 2
 KERNEL_ATTENTION_MFMA, KERNEL_ATTENTION_ROWS, KERNEL_ATTENTION_GENERIC = 3, 4, 5
-SPLITS_STATIC, SPLITS_IN_KERNEL, SPLITS_SCHEDULE = 0, 1, 2
+SPLITS_STATIC, SPLITS_IN_KERNEL, SPLITS_SCHEDULE, SPLITS_TILES = 0, 1, 2, 3
 
 EXPORTS = ("solve", "kv_int8_split_launch", "kv_int8_simple_launch", "kvq_decode_workspace_size",
            "kvq_workspace_init", "kvq_decode_launch", "kvq_append_launch", "kvq_quantize_rows_launch",

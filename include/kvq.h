@@ -322,6 +322,8 @@ const char* kvq_version(void);
 #define KVQ_SPLITS_STATIC 0     /* splits and chunk fixed on the host */
 #define KVQ_SPLITS_IN_KERNEL 1  /* ragged batch planned inside the decode kernel */
 #define KVQ_SPLITS_SCHEDULE 2   /* ragged batch planned by a schedule launch */
+#define KVQ_SPLITS_TILES 3      /* ragged batch as one tile stream, split evenly over the
+                                   matrix-core kernel's waves inside the kernel */
 
 typedef struct kvq_plan_info {
     int kernel;             /* KVQ_KERNEL_* */

@@ -164,7 +164,7 @@ def test_matrix_core_plan_by_workspace(L, B):
     S = 256 // Hkv
     flat = 4 * B >= S and (B <= 64 or B * (cap // 32) <= 16 * 4 * S)
     if flat or B <= 64:
-        assert info.split_plan == kvq.SPLITS_IN_KERNEL
+        assert info.split_plan == (kvq.SPLITS_TILES if flat else kvq.SPLITS_IN_KERNEL)
         items = 4 * S + B if flat else S
         assert n == 256 * 1024 + _ru(items * Hq * 2 * 4) + _ru(items * Hq * d * 4)
     else:
@@ -387,7 +387,7 @@ def test_decode_plan_kernels(L):
 
     assert plan(8, 32, 32, 128, 4096).kernel == kvq.KERNEL_DECODE_VALU           # cfg1
     i = plan(16, 32, 8, 128, 8192, lengths=A)                                    # cfg2
-    assert (i.kernel, i.heads_per_group, i.split_plan) == (kvq.KERNEL_DECODE_MFMA, 4, kvq.SPLITS_IN_KERNEL)
+    assert (i.kernel, i.heads_per_group, i.split_plan) == (kvq.KERNEL_DECODE_MFMA, 4, kvq.SPLITS_TILES)
     i = plan(1, 32, 8, 128, 131072)                                              # cfg3
     assert (i.kernel, i.split_plan, i.splits) == (kvq.KERNEL_DECODE_MFMA, kvq.SPLITS_STATIC, 32)
     i = plan(256, 64, 8, 128, 4096, lengths=A)                                   # cfg4

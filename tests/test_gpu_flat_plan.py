@@ -51,7 +51,7 @@ def _plan(B, Hq, Hkv, d, cap):
 
 def _check(o, B, Hkv, G, cap, d, lengths, rng, append=False, dist="normal", what=""):
     info = _plan(B, Hkv * G, Hkv, d, cap)
-    assert (info.kernel, info.split_plan) == (kvq.KERNEL_DECODE_MFMA, kvq.SPLITS_IN_KERNEL), what
+    assert (info.kernel, info.split_plan) == (kvq.KERNEL_DECODE_MFMA, kvq.SPLITS_TILES), what
     # the flattened plan: records for 4 waves per workgroup plus B ids per query head
     units = Hkv * (G // (8 if G % 8 == 0 else 4))
     S = 256 // units
