@@ -102,8 +102,8 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const Pre
     const buf_rsrc srs = make_rsrc(a.start, a.start ? static_cast<unsigned>(a.nseq) * 4u : 0u);
     const int start0 = a.start ? 0 : a.uniform_start;
     const bool paged = a.pages.table != nullptr;
-    const size_t tbytes = paged ? static_cast<size_t>(a.nseq) * a.pages.max_pages * 4 : 0;
-    const buf_rsrc trs = make_rsrc(a.pages.table, static_cast<unsigned>(min(tbytes, static_cast<size_t>(0x7fffffff))));
+    // Both fit in 2^31 bytes (the launcher sends larger tables to the generic kernel).
+    const buf_rsrc trs = make_rsrc(a.pages.table, paged ? static_cast<unsigned>(a.nseq) * a.pages.max_pages * 4u : 0u);
     for (unsigned r0 = (blockIdx.x * kPrefillWaves + wave) * RPW * kPrefillU; r0 < a.rows; r0 += step) {
         // The kPrefillU row loads go out together and unconditionally (a row
         // past the end rereads the last row and is dropped below), so no

@@ -902,7 +902,12 @@ hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t 
     a.divH = kvq::make_fastdiv(static_cast<uint32_t>(p->num_kv_heads));
     a.rows = static_cast<unsigned>(rows);
     a.planes = 2;
-    const bool vec_ok = aligned16(p->k_new) && aligned16(p->v_new) &&
+    // The tuned kernel reads start[] and the block table through buffer
+    // resources with 32-bit byte offsets; larger tables take the generic one.
+    const bool tables_fit = static_cast<long long>(p->batch) * 4 < (1LL << 31) &&
+                            (!p->block_table ||
+                             static_cast<long long>(p->batch) * p->max_pages_per_seq * 4 < (1LL << 31));
+    const bool vec_ok = tables_fit && aligned16(p->k_new) && aligned16(p->v_new) &&
                         ((reinterpret_cast<uintptr_t>(p->k_cache) | reinterpret_cast<uintptr_t>(p->v_cache)) & 7u) == 0;
     return finish_call(kvq::launch_prefill(a, p->head_dim, p->dtype == KVQ_DTYPE_BF16, vec_ok, stream), stream);
 }
