@@ -1098,17 +1098,27 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         for (int c = 0; c < NB; c++) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     };
 
-    // One wave's arrival for sequence b (lane 0; after the wave's record
-    // stores have completed): returns b when it completes the count of waves
-    // covering b, which then owns b's merge; the counter goes back to 0.
-    auto arrive = [&](int b, int bE, int bn) {
+    // One wave's arrival for sequence b, in two halves so that the wave does
+    // not wait for the atomic's return: arrive_issue (lane 0; after the
+    // wave's record stores have completed) bumps the counter and keeps the
+    // count it reached; arrive_resolve, after the tile loop, returns b when
+    // that count completes the number of waves covering b -- this wave then
+    // owns b's merge, and puts the counter back to 0 for the next launch.
+    auto arrive_issue = [&](int b) {
+        int reached = 0;
+        if (lane == 0) {
+            int* ctr = a.counters + static_cast<size_t>(b) * U + unit;
+            reached = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+        }
+        return reached;
+    };
+    auto arrive_resolve = [&](int b, int bE, int bn, int reached) {
         int done = -1;
         if (lane == 0) {
             const int cover = flat_wave_of(fs, bE + bn - 1) - flat_wave_of(fs, bE) + 1;
-            int* ctr = a.counters + static_cast<size_t>(b) * U + unit;
-            const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (prev + 1 == cover) {
-                __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next launch
+            if (reached == cover) {
+                __hip_atomic_store(a.counters + static_cast<size_t>(b) * U + unit, 0, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
                 done = b;
             }
         }
@@ -1118,7 +1128,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // Compute cursor (sequence of the tile being computed) and load cursor
     // (sequence of the tile being loaded, one ahead); wave-uniform.
     int pend = -1, pend_e = 0, pend_n = 0;  // this wave's partial first-segment record, not yet counted
-    int pm = -1, pm_e = 0, pm_n = 0;        // a sequence this wave completed mid-range (merged at the end)
+    bool pend_aged = false;                 // ... written at least one tile ago
+    int pm = -1, pm_e = 0, pm_n = 0, pm_reached = 0;  // that record's arrival, issued mid-range
     int cb = -1, cE = 0, cn = 0, clen = 0;
     int from = tb;  // first tile of the current segment
     const int ntiles = te - tb;
@@ -1161,7 +1172,13 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             if (more && t == cE + cn - 1) {
                 // The segment ends inside the range: a middle segment is a
                 // whole sequence, the first one may be a sequence's tail.
+                // The next sequence's q limbs come first: their loads went out
+                // with the next tile's, so that wait covers loads only.  After
+                // the segment's stores it would also wait for them to complete
+                // (the compiler cannot count loads past pending stores), which
+                // cost each switching wave ~2 us.
                 const bool complete = from == cE;
+                prepare_q();
                 emit_segment(cb, complete);
                 if (!complete) pend = cb, pend_e = cE, pend_n = cn;
                 cb = lb;
@@ -1170,18 +1187,23 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
                 clen = plan_len(cb);
                 from = t + 1;
                 reset_state();
-                prepare_q();
             }
             if (more) stage_v(Tn, s_v[wv][(it + 1) & 1]);
             if (pend >= 0) {
-                // Count the tail record now: the waits above have drained this
-                // wave's memory operations nearly (the record stores were
-                // issued before the next tile's last loads).
-                __builtin_amdgcn_s_waitcnt(0);
-                pm = arrive(pend, pend_e, pend_n);
-                pm_e = pend_e;
-                pm_n = pend_n;
-                pend = -1;
+                // Count the tail record one tile after it was written: by then
+                // its stores have completed and the wait below only covers
+                // loads the tile just staged has drained, so the tile pipeline
+                // does not stall (counting it at once cost such a wave ~3 us).
+                if (pend_aged) {
+                    __builtin_amdgcn_s_waitcnt(0);
+                    pm_reached = arrive_issue(pend);
+                    pm = pend;
+                    pm_e = pend_e;
+                    pm_n = pend_n;
+                    pend = -1;
+                } else {
+                    pend_aged = true;
+                }
             }
         };
         int it = 0;
@@ -1199,11 +1221,16 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     if (ntiles == 0) return;
     const bool last_done = from == cE && te == cE + cn;
     emit_segment(cb, last_done);
-    int done1 = -1;
-    if (!last_done) {
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's record stores have completed
-        done1 = arrive(cb, cE, cn);
+    if (!last_done || pend >= 0) __builtin_amdgcn_s_waitcnt(0);  // this wave's record stores have completed
+    if (pend >= 0) {  // a tail record written at the range's second-to-last tile
+        pm_reached = arrive_issue(pend);
+        pm = pend;
+        pm_e = pend_e;
+        pm_n = pend_n;
     }
+    const int last_reached = last_done ? 0 : arrive_issue(cb);
+    if (pm >= 0) pm = arrive_resolve(pm, pm_e, pm_n, pm_reached);
+    const int done1 = last_done ? -1 : arrive_resolve(cb, cE, cn, last_reached);
     if (pm < 0 && done1 < 0) return;
 #pragma unroll
     for (int k = 0; k < 2; k++) {
