@@ -738,9 +738,40 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         return lo + static_cast<int>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < step && s_E[i2] <= t &&
                                                                                     lo + lane < B))) - 1;
     };
-    const FlatSplit fs = flat_split(T, Wn);
-    const int tb = flat_start(fs, gw);
-    const int te = flat_start(fs, gw + 1);
+    // The waves split a virtual stream in which every sequence is preceded by
+    // kFlatSwitchTiles tiles of no work: sequence b's real tiles E_b + i sit at
+    // virtual position E_b + i + kFlatSwitchTiles * (b + 1).  A wave whose
+    // range crosses into a sequence gets that many fewer real tiles, which
+    // pays for the switch (the next sequence's q, the record of the one it
+    // leaves): ~2 us, by per-wave timestamps at cfg2.
+    const int P = kFlatSwitchTiles;
+    const FlatSplit fs = flat_split(T + P * B, Wn);
+    // The real tile at or after virtual position v (T at the end).
+    auto real_of = [&](int v) {
+        if (v >= T + P * B) return T;
+        int b, e, n;
+        if (!big) {
+            b = static_cast<int>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < B && e_l + P * lane <= v))) - 1;
+            e = __builtin_amdgcn_readlane(e_l, b);
+            n = __builtin_amdgcn_readlane(n_l, b);
+        } else {
+            const int step = (B + kWave - 1) / kWave;
+            const int i1 = min(B - 1, lane * step);
+            const int j1 = static_cast<int>(__builtin_popcountll(
+                               __builtin_amdgcn_ballot_w64(s_E[i1] + P * i1 <= v && lane * step < B))) - 1;
+            const int lo = j1 * step;
+            const int i2 = min(B - 1, lo + lane);
+            b = lo + static_cast<int>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(
+                         lane < step && s_E[i2] + P * i2 <= v && lo + lane < B))) - 1;
+            e = s_E[b];
+            n = s_E[b + 1] - e;
+        }
+        return e + min(max(v - e - P * (b + 1), 0), n);
+    };
+    // The wave holding real tile t of sequence b.
+    auto wave_of = [&](int t, int b) { return flat_wave_of(fs, t + P * (b + 1)); };
+    const int tb = real_of(flat_start(fs, gw));
+    const int te = real_of(flat_start(fs, gw + 1));
     if (big) win_load(tb < T ? find_seq(tb) : 0);
     auto seq_of = [&](int t) {  // the sequence holding tile t < T; moves the window when t is past it
         if (big && t >= wend) win_load(find_seq(t));
@@ -1115,7 +1146,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     auto arrive_resolve = [&](int b, int bE, int bn, int reached) {
         int done = -1;
         if (lane == 0) {
-            const int cover = flat_wave_of(fs, bE + bn - 1) - flat_wave_of(fs, bE) + 1;
+            const int cover = wave_of(bE + bn - 1, b) - wave_of(bE, b) + 1;
             if (reached == cover) {
                 __hip_atomic_store(a.counters + static_cast<size_t>(b) * U + unit, 0, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
@@ -1238,8 +1269,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         if (b < 0) continue;
         const int bE = k == 0 ? pm_e : cE;
         const int bn = k == 0 ? pm_n : cn;
-        const int w0 = flat_wave_of(fs, bE);
-        const int w1 = flat_wave_of(fs, bE + bn - 1);
+        const int w0 = wave_of(bE, b);
+        const int w1 = wave_of(bE + bn - 1, b);
         merge_wave_records<D, G>(a, b, w0, w1 - w0 + 1, hq0, lane);
     }
 }

@@ -85,6 +85,12 @@ constexpr int kMfmaTile = 32;
 // Most sequences of a ragged batch under the flattened tile plan of the
 // matrix-core kernel (their first tiles and lengths are scanned into LDS).
 constexpr int kFlatMaxSeqs = 4096;
+// Virtual tiles of no work before each sequence in the flattened tile plan
+// (the cost of a wave's switch into a sequence, in tiles).
+#ifndef KVQ_FLAT_SWITCH_TILES
+#define KVQ_FLAT_SWITCH_TILES 2
+#endif
+constexpr int kFlatSwitchTiles = KVQ_FLAT_SWITCH_TILES;
 
 // Which decode kernel a plan runs.
 enum class Kernel {
