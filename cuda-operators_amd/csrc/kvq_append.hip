@@ -63,13 +63,14 @@ __device__ __forceinline__ float load_elem(const void* row, int e) {
     else return static_cast<const float*>(row)[e];
 }
 
-// Max over aligned groups of N lanes (N a power of two <= 64).
+// Max over aligned groups of N lanes (N a power of two <= 64) of the lanes'
+// |x| maxima (non-negative; fmaxf drops NaN elements, so never NaN).
 template <int N>
 __device__ __forceinline__ float lanes_max(float x) {
     if constexpr (N <= 16) {
-        return group_max<N>(x);
+        return group_max_nonneg<N>(x);
     } else {
-        x = group_max<16>(x);
+        x = group_max_nonneg<16>(x);
         x = fmaxf(x, __shfl_xor(x, 16));
         if constexpr (N == 64) x = fmaxf(x, __shfl_xor(x, 32));
         return x;
@@ -77,17 +78,25 @@ __device__ __forceinline__ float lanes_max(float x) {
 }
 
 // Tuned path: LPR lanes read one row with a 16-byte load each (fp32: 4
-// elements, bf16: 8), so one wave load covers 64 / LPR whole rows; kPrefillU
-// wave loads are in flight per lane.  Each lane packs its quantised elements
-// into one 4- or 8-byte store, so a row's int8 bytes go out contiguous.
+// elements, bf16: 8), so one wave load covers 64 / LPR whole rows; U wave
+// loads are in flight per lane (fp32: 8, bf16: 4).  Each lane packs its
+// quantised elements into one 4- or 8-byte store, so a row's int8 bytes go
+// out contiguous.  The grid covers all rows in one pass up to
+// kPrefillMaxGroups workgroups: a workgroup takes one contiguous block of
+// rows, so the resident workgroups read and write one moving window of the
+// input and the cache (a grid-stride loop over 8192 workgroups, every
+// workgroup a quarter of the rows apart, was 10% slower for fp32).
 constexpr int kPrefillWaves = 4;
-constexpr int kPrefillU = 4;
+constexpr unsigned kPrefillMaxGroups = 1u << 20;
+template <bool BF16>
+constexpr int prefill_unroll() { return BF16 ? 4 : 8; }
 
 template <int D, bool BF16>
 __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const PrefillArgs a) {
     constexpr int EPL = BF16 ? 8 : 4;
     constexpr int LPR = D / EPL;
     constexpr int RPW = kWave / LPR;
+    constexpr int kPrefillU = prefill_unroll<BF16>();
     static_assert(LPR >= 1 && LPR <= kWave && (kWave % LPR) == 0, "row geometry");
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -241,7 +250,8 @@ hipError_t launch_prefill_t(const PrefillArgs& a, int d, bool vec_ok, hipStream_
     const unsigned want_rows = static_cast<unsigned>(a.rows);
     auto grid_for = [&](unsigned rows_per_wg) {
         const unsigned wgs = (want_rows + rows_per_wg - 1) / rows_per_wg;
-        return dim3(wgs < 8192 ? (wgs ? wgs : 1) : 8192, static_cast<unsigned>(a.planes));
+        const unsigned cap = a.max_groups ? min(a.max_groups, kPrefillMaxGroups) : kPrefillMaxGroups;
+        return dim3(wgs < cap ? (wgs ? wgs : 1) : cap, static_cast<unsigned>(a.planes));
     };
     const dim3 block(kPrefillWaves * kWave);
     constexpr int EPL = BF16 ? 8 : 4;
@@ -250,7 +260,7 @@ hipError_t launch_prefill_t(const PrefillArgs& a, int d, bool vec_ok, hipStream_
 #define KVQ_PREFILL_CASE(DD)                                                                        \
     case DD:                                                                                        \
         hipLaunchKernelGGL((prefill_kernel<DD, BF16>),                                              \
-                           grid_for(kPrefillWaves * (kWave / (DD / EPL)) * kPrefillU), block, 0,    \
+                           grid_for(kPrefillWaves * (kWave / (DD / EPL)) * prefill_unroll<BF16>()), block, 0, \
                            stream, a);                                                              \
         return hipGetLastError();
             KVQ_PREFILL_CASE(32)

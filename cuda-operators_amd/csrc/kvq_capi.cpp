@@ -86,6 +86,9 @@ size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // * KVQ_FORCE_KERNEL: "valu" keeps decode plans off the matrix-core kernel,
 //   "generic" off both tuned kernels, so one problem can be profiled on either
 //   kernel.  Any other value changes nothing.
+// * KVQ_PREFILL_MAX_GROUPS: a positive integer caps the prefill quantiser's
+//   workgroups per plane (default and maximum 2^20), so tests can run its
+//   grid-stride loop on small inputs.
 bool env_on(const char* name) {
     const char* s = getenv(name);
     if (!s) return false;
@@ -110,6 +113,17 @@ bool flat_enabled() {
         return !(s && strcmp(s, "0") == 0);
     }();
     return on;
+}
+
+unsigned prefill_max_groups() {
+    static const unsigned g = [] {
+        const char* s = getenv("KVQ_PREFILL_MAX_GROUPS");
+        if (!s || !*s) return 0u;
+        char* end = nullptr;
+        const long v = strtol(s, &end, 10);
+        return (*end == '\0' && v > 0 && v <= (1L << 20)) ? static_cast<unsigned>(v) : 0u;
+    }();
+    return g;
 }
 
 int forced_kernel() {
@@ -805,6 +819,7 @@ hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, 
         a.planes = 1;
         a.nseq = 1;
         a.pages = kvq::PageMap{nullptr, 0, 0, 0, -1};
+        a.max_groups = prefill_max_groups();
         return finish_call(kvq::launch_prefill(a, head_dim, false, true, stream), stream);
     }
     return finish_call(kvq::launch_quantize_rows(x, rows, head_dim, q, scale, stream), stream);
@@ -902,6 +917,7 @@ hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t 
     a.divH = kvq::make_fastdiv(static_cast<uint32_t>(p->num_kv_heads));
     a.rows = static_cast<unsigned>(rows);
     a.planes = 2;
+    a.max_groups = prefill_max_groups();
     // The tuned kernel reads start[] and the block table through buffer
     // resources with 32-bit byte offsets; larger tables take the generic one.
     const bool tables_fit = static_cast<long long>(p->batch) * 4 < (1LL << 31) &&

@@ -46,6 +46,20 @@ __device__ __forceinline__ float group_max(float x) {
     return x;
 }
 
+// Max over aligned groups of N lanes of non-negative, non-NaN floats.  Their
+// bit patterns order as unsigned integers, so the steps run as v_max_u32 with
+// the DPP operand folded in (the float max needs a quieting step per stage).
+template <int N>
+__device__ __forceinline__ float group_max_nonneg(float x) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group size");
+    unsigned u = __float_as_uint(x);
+    if constexpr (N >= 2) u = max(u, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u), kDppQuadXor1, 0xF, 0xF, false)));
+    if constexpr (N >= 4) u = max(u, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u), kDppQuadXor2, 0xF, 0xF, false)));
+    if constexpr (N >= 8) u = max(u, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u), kDppRowHalfMirror, 0xF, 0xF, false)));
+    if constexpr (N >= 16) u = max(u, static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(u), kDppRowMirror, 0xF, 0xF, false)));
+    return __uint_as_float(u);
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
@@ -127,7 +141,18 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // -127, 127) with rintf = round half to even (v_rndne_f32); a zero scale (amax
 // == 0, or amax so small that the quotient underflows) stores q = 0.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float quant_scale(float amax) { return amax / 127.0f; }
+// RN(amax / 127) without the divide: with C = 1/127 split as Ch = RN(C) and
+// Cl = RN(C - Ch), fma(amax, Ch, RN(amax * Cl)) is the correctly rounded
+// quotient for every amax >= 2^-112 (Brisebarre and Muller, "Correctly rounded
+// multiplication by arbitrary precision constants", IEEE TC 57(2), 2008; for
+// this C checked over all such floats by tests/quant_scale_check.c).  Smaller
+// amax (a subnormal or near-subnormal quotient) takes the divide.
+__device__ __forceinline__ float quant_scale(float amax) {
+    constexpr float kCh = 0x1.020408p-7f;
+    constexpr float kCl = 0x1.020408p-35f;
+    if (__builtin_expect(amax < 0x1p-112f, 0)) return amax / 127.0f;
+    return __builtin_fmaf(amax, kCh, amax * kCl);
+}
 
 __device__ __forceinline__ int quant_one(float x, float scale) {
     if (scale == 0.0f) return 0;
@@ -151,27 +176,32 @@ __device__ __forceinline__ int quant_one(float x, float scale) {
 //   the same side and is not itself a tie).  The test also holds when the
 //   compiler fuses y - n into fma(x, rinv, -n): then it measures the exact
 //   product P, with |P - Q| <= 1.5 * 2^-16 and |y - P| <= 2^-17, both below
-//   the margin, so q, P and Q round alike.  Lanes with an element within
-//   2^-15 of one (about one element in 16000), or with a scale outside
-//   [2^-100, 2^100] (zero, subnormal or non-finite scales included), redo the
-//   row part with quant_one.
-// Cost per element: multiply, rint, subtract, compare, clamp, convert --
+//   the margin, so q, P and Q round alike.  An element within 2^-15 of a
+//   half-integer takes quant_one: about one in 16000 for fp32 data, but about
+//   one in 600 for bf16 inputs, whose 8-bit significands often make x / scale
+//   an exact tie.  So does every element of a row whose scale is outside
+//   [2^-100, 2^100] (zero, subnormal or non-finite scales included).
+// * No clamp is needed on the fast path: |x| <= amax gives |q| < 127.001, so
+//   rintf(q) is within [-127, 127].
+// Cost per element: multiply, rint, fused subtract, compare, convert --
 // against the IEEE divide's ten instructions.
 template <int N>
 __device__ __forceinline__ void quant_row(const float (&x)[N], float scale, int (&q)[N]) {
-    const bool normal = scale >= 0x1p-100f && scale <= 0x1p100f;
-    const float rinv = __builtin_amdgcn_rcpf(normal ? scale : 1.0f);
-    float dmax = 0.0f;  // largest |y - rint(y)| of the lane's elements
+    if (!(scale >= 0x1p-100f && scale <= 0x1p100f)) {
+#pragma unroll
+        for (int i = 0; i < N; i++) q[i] = quant_one(x[i], scale);
+        return;
+    }
+    const float rinv = __builtin_amdgcn_rcpf(scale);
 #pragma unroll
     for (int i = 0; i < N; i++) {
         const float y = x[i] * rinv;
         const float n = __builtin_rintf(y);
-        dmax = fmaxf(dmax, fabsf(y - n));
-        q[i] = static_cast<int>(fminf(fmaxf(n, -127.0f), 127.0f));
-    }
-    if (!normal || dmax >= 0.5f - 0x1p-15f) {
-#pragma unroll
-        for (int i = 0; i < N; i++) q[i] = quant_one(x[i], scale);
+        q[i] = static_cast<int>(n);
+        // One branch per element, so a wave runs the divide only for the
+        // element positions that some lane flags.  A NaN element fails the
+        // test and takes quant_one too.
+        if (!(fabsf(y - n) < 0.5f - 0x1p-15f)) q[i] = quant_one(x[i], scale);
     }
 }
 

@@ -154,6 +154,7 @@ struct PrefillArgs {
     int planes;  // 2: K and V; 1: K only
     int nseq;    // sequences (entries of start, rows of the page table)
     PageMap pages;
+    unsigned max_groups;  // grid cap per plane (0: the default); beyond it workgroups stride
 };
 // vec_ok: 16-byte aligned inputs and 8-byte aligned caches (tuned kernel for
 // d in {32, 64, 128, 256}).

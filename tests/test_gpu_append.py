@@ -211,3 +211,76 @@ def test_append_cfg4_shape():
     o.append(kn, vn, k, v, ks, vs, positions=pos)
     assert np.array_equal(down(gk), k) and np.array_equal(down(gv), v)
     assert np.array_equal(_bits(down(gks)), _bits(ks)) and np.array_equal(_bits(down(gvs)), _bits(vs))
+
+
+def tiny_scale_rows(rng, d, rows):
+    """Rows whose amax spans 2^-126 .. 2^-80 (denser around 2^-112, below
+    which the device's scale takes the IEEE divide, and up to 2^-90, where
+    amax * Cl of its divide-free scale is subnormal), random significands."""
+    e = np.concatenate([rng.uniform(-126.0, -80.0, rows // 2), rng.uniform(-114.0, -110.0, rows - rows // 2)])
+    amax = (np.float32(2.0) ** e.astype(np.float32)) * rng.uniform(1.0, 2.0, rows).astype(np.float32)
+    x = rng.uniform(-1.0, 1.0, (rows, d)).astype(np.float32) * amax[:, None]
+    x[np.arange(rows), rng.integers(0, d, rows)] = amax * np.where(np.arange(rows) % 2 == 0, 1, -1)
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_quantize_tiny_scales_bit_exact(d):
+    """Scales near and below the range of the divide-free scale computation:
+    scale bits and int8 values equal the oracle's, fp32 rows through
+    quantize_rows and bf16 rows through prefill."""
+    o = orc.get()
+    x = tiny_scale_rows(np.random.default_rng(300 + d), d, 4096)
+    gq, gs = kvq.quantize_rows(up(x))
+    torch.cuda.synchronize()
+    wq, ws = o.quantize_rows(x)
+    assert np.array_equal(_bits(down(gs)), _bits(ws))
+    assert np.array_equal(down(gq), wq)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    k = torch.zeros((1, 1, x.shape[0], d), dtype=torch.int8, device="cuda")
+    ks = torch.zeros((1, 1, x.shape[0]), dtype=torch.float32, device="cuda")
+    kvq.prefill(xb.view(1, 1, -1, d).cuda(), xb.view(1, 1, -1, d).cuda(), k, k.clone(), ks, ks.clone())
+    torch.cuda.synchronize()
+    bq, bs = o.quantize_rows(xb.to(torch.float32).numpy())
+    assert np.array_equal(_bits(down(ks)[0, 0]), _bits(bs)) and np.array_equal(down(k)[0, 0], bq)
+
+
+_STRIDE_CHILD = r"""
+import sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[1] + "/tests")
+from _gpu import down, kvq, up
+from oracle import oracle as orc
+o = orc.get()
+rng = np.random.default_rng(11)
+for dt in (torch.float32, torch.bfloat16):
+    for d in (64, 128):
+        x = (rng.standard_normal((3, 2, 1000, d), dtype=np.float32) * 3).astype(np.float32)
+        xt = torch.from_numpy(x).to(dt)
+        k = torch.zeros((3, 2, 1000, d), dtype=torch.int8, device="cuda")
+        ks = torch.zeros((3, 2, 1000), dtype=torch.float32, device="cuda")
+        v, vs = k.clone(), ks.clone()
+        kvq.prefill(xt.cuda(), (-xt).cuda(), k, v, ks, vs)
+        torch.cuda.synchronize()
+        xf = xt.to(torch.float32).numpy().reshape(-1, d)
+        wq, ws = o.quantize_rows(xf)
+        nq, ns = o.quantize_rows(-xf)
+        assert np.array_equal(down(k).reshape(-1, d), wq) and np.array_equal(down(ks).reshape(-1), ws)
+        assert np.array_equal(down(v).reshape(-1, d), nq) and np.array_equal(down(vs).reshape(-1), ns)
+print("stride ok")
+"""
+
+
+def test_prefill_grid_stride_loop():
+    """The prefill quantiser with its grid capped at 3 workgroups per plane
+    (KVQ_PREFILL_MAX_GROUPS, read once per process, hence a child process):
+    every workgroup walks the rows of both planes in strides, bit-exact."""
+    import subprocess
+    import sys
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, KVQ_PREFILL_MAX_GROUPS="3")
+    r = subprocess.run([sys.executable, "-c", _STRIDE_CHILD, repo], env=env, capture_output=True, text=True,
+                       timeout=110)
+    assert r.returncode == 0 and "stride ok" in r.stdout, (r.stdout + r.stderr)[-3000:]
