@@ -32,35 +32,44 @@
 namespace kvq {
 namespace {
 
-constexpr int kSchedThreads = 1024;
+// 256 threads: at B256 the 1024-thread version took 5.9 us per launch and
+// this one 4.8 us (fewer waves in every barrier and scan); 64 and 128
+// threads, which loop more, took 8.7 and 6.4 us.
+constexpr int kSchedThreads = 256;
+constexpr int kSchedLen = 1024;  // lengths kept in LDS
 constexpr int kSchedWaves = kSchedThreads / kWave;
 constexpr int kSizeClasses = 64;
+
+// Inclusive prefix sum over the wave: Hillis-Steele steps within each
+// 16-lane row (DPP row_shr 1, 2, 4, 8; lanes shifted in from outside the row
+// add 0), then the row broadcasts of GFX9 DPP: lane 15 of rows 0 and 2 into
+// rows 1 and 3 (row_bcast:15), lane 31 into rows 2 and 3 (row_bcast:31).
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return v;
+}
 
 // Exclusive prefix sum of x over the workgroup (thread order); *total gets
 // the sum.  s_tmp: kSchedWaves ints of LDS, reusable after the call.
 __device__ int block_exclusive_scan(int x, int* s_tmp, int* total) {
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    int v = x;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const int y = __shfl_up(v, off);
-        if (lane >= off) v += y;
-    }
+    const int v = wave_inclusive_scan(x);
     if (lane == kWave - 1) s_tmp[wave] = v;
     __syncthreads();
-    if (wave == 0) {
-        int u = lane < kSchedWaves ? s_tmp[lane] : 0;
+    int before = 0, all = 0;
 #pragma unroll
-        for (int off = 1; off < kSchedWaves; off <<= 1) {
-            const int y = __shfl_up(u, off);
-            if (lane >= off) u += y;
-        }
-        if (lane < kSchedWaves) s_tmp[lane] = u;
+    for (int w = 0; w < kSchedWaves; w++) {
+        const int t = s_tmp[w];
+        before += w < wave ? t : 0;
+        all += t;
     }
-    __syncthreads();
-    const int before = wave > 0 ? s_tmp[wave - 1] : 0;
-    *total = s_tmp[kSchedWaves - 1];
+    *total = all;
     __syncthreads();
     return before + v - x;
 }
@@ -83,20 +92,20 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
     __shared__ int s_tmp[kSchedWaves];
     __shared__ long long s_sum[kSchedWaves];
     __shared__ int s_class[kSizeClasses];
-    __shared__ int s_len[kSchedThreads];  // the first kSchedThreads clamped lengths
+    __shared__ int s_len[kSchedLen];  // the first kSchedLen clamped lengths
     __shared__ int s_best;
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
     const int wave = t / kWave;
     // Length of sequence b: from LDS after the first pass (one read of the
-    // lengths for batches up to kSchedThreads), from memory beyond that.
-    auto len_of = [&](int b) { return b < kSchedThreads ? s_len[b] : clamped_len(lengths, b, max_len); };
+    // lengths for batches up to kSchedLen), from memory beyond that.
+    auto len_of = [&](int b) { return b < kSchedLen ? s_len[b] : clamped_len(lengths, b, max_len); };
 
     long long sum = 0;
     for (int b = t; b < B; b += kSchedThreads) {
         const int len = clamped_len(lengths, b, max_len);
         sum += len;
-        if (b < kSchedThreads) s_len[b] = len;
+        if (b < kSchedLen) s_len[b] = len;
     }
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
@@ -113,7 +122,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
     const long long cmax = (static_cast<long long>(max(max_len, 1)) + gran - 1) / gran * gran;
     const int S = target / units;
 
-    if (B <= S && B <= kSchedThreads) {
+    if (B <= S && B <= kSchedLen) {
         // One round: the smallest chunk whose items all fit.
         const long long lo = min(cmax, max(static_cast<long long>(gran), (total + S - 1) / S + gran - 1) / gran * gran);
         const long long hi =
@@ -125,23 +134,28 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
         }
         __syncthreads();
         const int chunk = s_best;
-        int n = 0, cb = gran;
-        if (t < B) {
-            const int len = s_len[t];
-            n = len == 0 ? 1 : (len + chunk - 1) / chunk;
-            cb = len == 0 ? gran : ((len + n - 1) / n + gran - 1) / gran * gran;
-        }
-        int tot = 0;
-        const int pre = block_exclusive_scan(n, s_tmp, &tot);
-        if (t < B) {
-            seq[t] = make_int2(pre, cb);
-            for (int s = 0; s < n; s++) {
-                if (pre + s < items_cap) put_item(items, pre + s, t, s, n, pre, cb, s_len[t]);
+        int carry = 0;
+        for (int b0 = 0; b0 < B; b0 += kSchedThreads) {
+            const int b = b0 + t;
+            int n = 0, cb = gran;
+            if (b < B) {
+                const int len = s_len[b];
+                n = len == 0 ? 1 : (len + chunk - 1) / chunk;
+                cb = len == 0 ? gran : ((len + n - 1) / n + gran - 1) / gran * gran;
             }
+            int tot = 0;
+            const int pre = carry + block_exclusive_scan(n, s_tmp, &tot);
+            if (b < B) {
+                seq[b] = make_int2(pre, cb);
+                for (int s = 0; s < n; s++) {
+                    if (pre + s < items_cap) put_item(items, pre + s, b, s, n, pre, cb, s_len[b]);
+                }
+            }
+            carry += tot;
         }
         if (t == 0) {
             sched[0] = chunk;
-            sched[1] = min(tot, items_cap);
+            sched[1] = min(carry, items_cap);
         }
         return;
     }
@@ -158,9 +172,13 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
             n = len == 0 ? 1 : (len + chunk - 1) / chunk;
         }
         const int full = n > 0 ? n - 1 : 0;
-        int tot_n = 0, tot_f = 0;
+        // Every b < B has n >= 1, so the prefix of the full chunks is the
+        // prefix of n less the sequences before b in this pass.
+        int tot_n = 0;
         const int pre_n = block_exclusive_scan(n, s_tmp, &tot_n);
-        const int pre_f = block_exclusive_scan(full, s_tmp, &tot_f);
+        const int valid = min(B - b0, kSchedThreads);
+        const int pre_f = pre_n - t;
+        const int tot_f = tot_n - valid;
         if (b < B) {
             seq[b] = make_int2(rec_carry + pre_n, chunk);
             for (int s = 0; s < full; s++) {
@@ -178,13 +196,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
     // Size classes -> first item position of each class (longest first).
     if (wave == 0) {
         const int cnt = s_class[lane];
-        int v = cnt;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-            const int y = __shfl_up(v, off);
-            if (lane >= off) v += y;
-        }
-        s_class[lane] = full_carry + v - cnt;
+        s_class[lane] = full_carry + wave_inclusive_scan(cnt) - cnt;
     }
     __syncthreads();
     for (int b = t; b < B; b += kSchedThreads) {
