@@ -315,6 +315,140 @@ __global__ __launch_bounds__(W* kWave) void attention_mfma(const AttnArgs a) {
     }
 }
 
+// attention_direct<D, W>: 9 to 32 queries (16 per wave, W waves) on the
+// same v_mfma_f32_16x16x4_f32 products as attention_mfma, but with no LDS
+// tile and no padded 64-query block: each wave streams its split's keys from
+// global memory straight into its MFMA operands, 16 keys per block, the next
+// block loading while the current one is computed.  Per block a lane loads
+//   K[t + r][g * D/4 + s], s < D/4   (its A operand of S^T = K q^T), and
+//   V[t + 4 g + i][NB * r + c]        (its A operand of O^T += V^T P^T),
+// so every byte of the block is read once per wave, in 16-byte loads that
+// cover whole rows per lane group.  The W waves of a workgroup read the same
+// keys (L2 hits after the first).  Keys past the split's end read its last
+// row (in bounds); their scores are -inf and their V values zero.  Splits
+// write the (m, l, acc) records attention_merge combines, as attention_mfma.
+constexpr int kDirectBlock = 16;  // keys per block
+template <int D, int W>
+__global__ __launch_bounds__(W* kWave) void attention_direct(const AttnArgs a) {
+    constexpr int DQ = D / 4;
+    constexpr int NB = D / 16;
+    static_assert(NB % 4 == 0, "V operand width");
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int split = blockIdx.y;
+    const int q0 = blockIdx.x * (16 * W) + wave * 16;
+    const int k0 = split * a.chunk;
+    const int k1 = min(a.N, k0 + a.chunk);
+
+    float qv[DQ];
+    {
+        const float* qp = a.q + static_cast<size_t>(min(q0 + r, a.M - 1)) * D + g * DQ;
+#pragma unroll
+        for (int j = 0; j < DQ / 4; j++) {
+            const float4 x = *reinterpret_cast<const float4*>(qp + 4 * j);
+            qv[4 * j] = x.x * a.scale_log2;
+            qv[4 * j + 1] = x.y * a.scale_log2;
+            qv[4 * j + 2] = x.z * a.scale_log2;
+            qv[4 * j + 3] = x.w * a.scale_log2;
+        }
+    }
+    f32x4 o[NB];
+#pragma unroll
+    for (int c = 0; c < NB; c++) o[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+
+    struct Block {
+        float4 k[DQ / 4];
+        float4 v[4][NB / 4];
+    };
+    auto load_block = [&](int t, Block& b) {
+        const float* kr = a.k + static_cast<size_t>(min(t + r, k1 - 1)) * D + g * DQ;
+#pragma unroll
+        for (int j = 0; j < DQ / 4; j++) b.k[j] = *reinterpret_cast<const float4*>(kr + 4 * j);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float* vr = a.v + static_cast<size_t>(min(t + 4 * g + i, k1 - 1)) * D + NB * r;
+#pragma unroll
+            for (int j = 0; j < NB / 4; j++) b.v[i][j] = *reinterpret_cast<const float4*>(vr + 4 * j);
+        }
+    };
+
+    Block cur;
+    load_block(k0, cur);
+    for (int t = k0; t < k1; t += kDirectBlock) {
+        Block nxt;
+        load_block(t + kDirectBlock, nxt);  // unconditional: past k1 it rereads the last row
+        f32x4 c = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < DQ / 4; j++) {
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[j].x, qv[4 * j], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[j].y, qv[4 * j + 1], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[j].z, qv[4 * j + 2], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(cur.k[j].w, qv[4 * j + 3], c, 0, 0, 0);
+        }
+        // sv[i]: score of key t + 4 g + i for query r.
+        float sv[4];
+        bool live[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            live[i] = t + 4 * g + i < k1;
+            sv[i] = live[i] ? c[i] : -INFINITY;
+        }
+        float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        const float ms = mn == -INFINITY ? 0.0f : mn;
+        const float alpha = fast_exp2(m - ms);
+        m = mn;
+        l *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            sv[i] = fast_exp2(sv[i] - ms);
+            l += sv[i];
+        }
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+            for (int cc = 0; cc < NB; cc++) o[cc] *= alpha;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int j = 0; j < NB / 4; j++) {
+                const float4 x = cur.v[i][j];
+                const float vv[4] = {live[i] ? x.x : 0.0f, live[i] ? x.y : 0.0f, live[i] ? x.z : 0.0f,
+                                     live[i] ? x.w : 0.0f};
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    o[4 * j + e] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[e], sv[i], o[4 * j + e], 0, 0, 0);
+            }
+        }
+        cur = nxt;
+    }
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+
+    const int q = q0 + r;
+    if (q < a.M) {
+        const bool whole = a.splits == 1;
+        const float inv = whole ? 1.0f / l : 1.0f;
+        float* const row = whole ? a.out + static_cast<size_t>(q) * D
+                                 : a.part_acc + (static_cast<size_t>(split) * a.M + q) * D;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float* op = row + NB * (4 * g + i);
+#pragma unroll
+            for (int c4 = 0; c4 < NB; c4 += 4)
+                *reinterpret_cast<float4*>(op + c4) =
+                    make_float4(o[c4][i] * inv, o[c4 + 1][i] * inv, o[c4 + 2][i] * inv, o[c4 + 3][i] * inv);
+        }
+        if (!whole && g == 0)
+            *reinterpret_cast<float2*>(a.part_ml + (static_cast<size_t>(split) * a.M + q) * 2) = make_float2(m, l);
+    }
+}
+
 // attention_rows<D, QM>: up to QM <= 8 queries (decode-shaped attention) on
 // the VALU, with no LDS tiles and no padded query block.  A key row is held by
 // a group of L lanes, each with E = D/L of its dims: float4 number j·L + lane
@@ -562,6 +696,7 @@ __global__ __launch_bounds__(kGenWaves* kWave) void attention_generic(const Attn
 int attention_tuned_dim(int d) { return d == 32 || d == 64 || d == 128 || d == 256; }
 int attention_key_tile(int d) { return d >= 256 ? attention_tile<256>() : attention_tile<128>(); }
 int attention_max_splits(int) { return kAttnMaxSplits; }
+int attention_direct_dim(int d) { return d == 64 || d == 128; }
 int attention_rows_queries(int M) {
     if (M <= 1) return 1;
     if (M <= 2) return 2;
@@ -607,11 +742,29 @@ void launch_rows_attention_d(const AttnArgs& a, int glog, hipStream_t stream) {
         default: launch_rows_attention<D, kRowsMaxQueries>(a, glog, stream); break;
     }
 }
+template <int D, int W>
+void launch_direct_attention(const AttnArgs& a, int glog, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((a.M + 16 * W - 1) / (16 * W)), static_cast<unsigned>(a.splits));
+    hipLaunchKernelGGL((attention_direct<D, W>), grid, dim3(W * kWave), 0, stream, a);
+    if (a.splits > 1) {
+        const dim3 mgrid(static_cast<unsigned>(
+            ((static_cast<long long>(a.M) * (D / 4) << glog) + kMergeThreads - 1) / kMergeThreads));
+        hipLaunchKernelGGL(attention_merge<D>, mgrid, dim3(kMergeThreads), 0, stream, a, glog);
+    }
+}
 template <int D>
 void launch_mfma_attention_d(const AttnArgs& a, int glog, hipStream_t stream) {
     if (a.qblock <= kRowsMaxQueries) {
         launch_rows_attention_d<D>(a, glog, stream);
         return;
+    }
+    if constexpr (D == 64 || D == 128) {
+        if (a.direct) {
+            if (a.qblock == 16) launch_direct_attention<D, 1>(a, glog, stream);
+            else if (a.qblock == 32) launch_direct_attention<D, 2>(a, glog, stream);
+            else launch_direct_attention<D, 4>(a, glog, stream);
+            return;
+        }
     }
     if constexpr (D <= 128) {  // at d = 256 a 4-wave block would need over 256 VGPRs
         if (a.qblock == kAttnBlockNarrow) {

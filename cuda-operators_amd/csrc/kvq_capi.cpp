@@ -573,8 +573,16 @@ DecodePlan paged_plan(const kvq_paged_decode_params* p) {
 // register file holds one per CU, below that two).
 int attention_target_workgroups(int d) { return d >= 128 ? 256 : 512; }
 
+// The register-direct attention kernel (9-64 queries, d = 64 or 128): key
+// splits per launch, KVQ_ATTN_DIRECT_SPLITS(M), but at least min(blocks, 128)
+// and at most half the 16-key blocks (two blocks per wave at the least).
+#ifndef KVQ_ATTN_DIRECT_SPLITS
+#define KVQ_ATTN_DIRECT_SPLITS(M) ((M) <= 16 ? 512 : 256)
+#endif
+
 struct AttnPlan {
     bool tuned = false;
+    bool direct = false;
     int splits = 1, chunk = 0;
     int qblock = kvq::kAttnBlockWide;
     size_t ml_bytes = 0, acc_bytes = 0;
@@ -593,12 +601,16 @@ AttnPlan attention_plan(int M, int N, int d, bool aligned, int requested) {
     p.tuned = kvq::attention_tuned_dim(d) && aligned;
     p.chunk = N;
     if (!p.tuned) return p;  // the generic kernel runs unsplit
-    // 9-16 queries over long key ranges also run the VALU kernel, as 8-query
-    // blocks (M = 16, N = 65536: 38 us at d = 128, 23.6 at d = 64, 65.9 at
-    // d = 256, against 45.7, 28.2, 83.3 us in a padded matrix-core block); at
-    // N = 16384 (23.2 vs 16.7 us) or 24+ queries the matrix cores win.
+    // 9-16 queries over long key ranges at d = 32 or 256 also run the VALU
+    // kernel, as 8-query blocks (M = 16, N = 65536, d = 256: 65.9 us against
+    // 83.3 us in a padded matrix-core block); at d = 64 and 128 the
+    // register-direct kernel below takes them.
     int qm = kvq::attention_rows_queries(M);
-    if (qm == 0 && M <= 2 * kvq::kAttnRowsBlock && N >= 65536) qm = kvq::kAttnRowsBlock;
+    // 9-64 queries: the register-direct kernel where it beat the other
+    // kernels (one box, see the attention notes): at d = 128 from 16384 keys,
+    // or with up to 32 queries at any key count; at d = 64 from 32768 keys.
+    const bool direct_ok = M <= 64 && kvq::attention_direct_dim(d) && (d == 128 ? (N >= 16384 || M <= 32) : N >= 32768);
+    if (qm == 0 && M <= 2 * kvq::kAttnRowsBlock && N >= 65536 && !direct_ok) qm = kvq::kAttnRowsBlock;
     if (qm > 0) {
         // A few queries: the VALU kernel, query blocks of qm, key splits to
         // fill KVQ_ATTN_ROWS_TARGET(qm) workgroups per query block.
@@ -609,6 +621,24 @@ AttnPlan attention_plan(int M, int N, int d, bool aligned, int requested) {
                                                                      : static_cast<long long>(KVQ_ATTN_ROWS_TARGET(qm)),
                                                       rtiles, static_cast<long long>(kvq::attention_max_splits(d))}));
         p.chunk = static_cast<int>(std::min<long long>((rtiles + want - 1) / want * rt, N));
+        p.splits = static_cast<int>((N + static_cast<long long>(p.chunk) - 1) / p.chunk);
+        if (p.splits > 1) {
+            p.ml_bytes = round_up(static_cast<size_t>(p.splits) * M * 2 * sizeof(float), kAlign);
+            p.acc_bytes = round_up(static_cast<size_t>(p.splits) * M * d * sizeof(float), kAlign);
+        }
+        return p;
+    }
+    if (direct_ok) {
+        // 16 queries per wave, 1, 2 or 4 waves per workgroup.
+        p.direct = true;
+        p.qblock = M <= 16 ? 16 : M <= 32 ? 32 : 64;
+        const long long blocks = (static_cast<long long>(N) + 15) / 16;
+        const long long cap = std::min<long long>(blocks, kvq::attention_max_splits(d));
+        const long long want =
+            requested > 0 ? std::min<long long>(requested, cap)
+                          : std::min(cap, std::max(std::min(blocks, 128LL),
+                                                   std::min<long long>(KVQ_ATTN_DIRECT_SPLITS(M), (blocks + 1) / 2)));
+        p.chunk = static_cast<int>(std::min<long long>((blocks + want - 1) / want * 16, N));
         p.splits = static_cast<int>((N + static_cast<long long>(p.chunk) - 1) / p.chunk);
         if (p.splits > 1) {
             p.ml_bytes = round_up(static_cast<size_t>(p.splits) * M * 2 * sizeof(float), kAlign);
@@ -663,6 +693,7 @@ hipError_t attention_run(int M, int N, int d, const float* q, const float* k, co
     a.chunk = p.chunk;
     a.qblock = p.qblock;
     a.tuned = p.tuned;
+    a.direct = p.direct;
     a.scale_log2 = scale * 1.4426950408889634f;
     if (p.splits > 1) {
         char* base = static_cast<char*>(ws);
@@ -979,6 +1010,7 @@ hipError_t kvq_attention_plan(const kvq_attention_params* p, kvq_plan_info* info
     kvq_plan_info r{};
     if (!plan.tuned) r.kernel = KVQ_KERNEL_ATTENTION_GENERIC;
     else if (plan.qblock <= kvq::kAttnRowsBlock) r.kernel = KVQ_KERNEL_ATTENTION_ROWS;
+    else if (plan.direct) r.kernel = KVQ_KERNEL_ATTENTION_DIRECT;
     else r.kernel = KVQ_KERNEL_ATTENTION_MFMA;
     r.heads_per_group = 1;
     r.splits = plan.splits;

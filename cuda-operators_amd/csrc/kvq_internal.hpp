@@ -180,6 +180,7 @@ struct AttnArgs {
     int splits, chunk;  // key splits (grid y) and keys per split (a multiple of the key tile)
     int qblock;         // queries per workgroup: kAttnBlockWide or kAttnBlockNarrow (matrix cores),
                         // or 1, 2, 4, 8 (few-query kernel, attention_rows)
+    bool direct;        // attention_direct: qblock 16, 32 or 64 queries (16 per wave), no LDS
     float scale_log2;   // softmax scale * log2(e)
     bool tuned;         // a tuned kernel runs (tuned head dim and 16-byte aligned q, k, v, out);
                         // otherwise attention_generic, unsplit
@@ -187,6 +188,7 @@ struct AttnArgs {
 int attention_tuned_dim(int d);   // the matrix-core kernel handles head dim d
 int attention_key_tile(int d);    // keys per LDS tile of the matrix-core kernel at head dim d
 int attention_max_splits(int d);  // most key splits per matrix-core launch (tuned d)
+int attention_direct_dim(int d);  // attention_direct handles head dim d
 int attention_rows_queries(int M);  // queries per workgroup of the few-query kernel (0: M too large)
 int attention_rows_tile(int d);     // keys per workgroup step of the few-query kernel (tuned d)
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);

@@ -110,7 +110,7 @@ class PlanInfo(ctypes.Structure):
 
 
 KERNEL_DECODE_GENERIC, KERNEL_DECODE_VALU, KERNEL_DECODE_MFMA = 0, 1, 2
-KERNEL_ATTENTION_MFMA, KERNEL_ATTENTION_ROWS, KERNEL_ATTENTION_GENERIC = 3, 4, 5
+KERNEL_ATTENTION_MFMA, KERNEL_ATTENTION_ROWS, KERNEL_ATTENTION_GENERIC, KERNEL_ATTENTION_DIRECT = 3, 4, 5, 6
 SPLITS_STATIC, SPLITS_IN_KERNEL, SPLITS_SCHEDULE, SPLITS_TILES = 0, 1, 2, 3
 
 EXPORTS = ("solve", "kv_int8_split_launch", "kv_int8_simple_launch", "kvq_decode_workspace_size",

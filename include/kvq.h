@@ -318,6 +318,7 @@ const char* kvq_version(void);
 #define KVQ_KERNEL_ATTENTION_MFMA 3   /* attention_mfma: query blocks on matrix cores */
 #define KVQ_KERNEL_ATTENTION_ROWS 4   /* attention_rows: up to 8 queries per workgroup */
 #define KVQ_KERNEL_ATTENTION_GENERIC 5 /* attention_generic: any head dim or alignment */
+#define KVQ_KERNEL_ATTENTION_DIRECT 6  /* attention_direct: 9-64 queries, 16 per wave, no LDS tiles */
 
 #define KVQ_SPLITS_STATIC 0     /* splits and chunk fixed on the host */
 #define KVQ_SPLITS_IN_KERNEL 1  /* ragged batch planned inside the decode kernel */

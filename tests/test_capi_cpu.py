@@ -292,10 +292,16 @@ def test_attention_workspace_plan(L):
     assert size(8, 32, 128) == 0  # one step of 32 keys
     assert size(3, 8192, 64, splits=1 << 20) == size(3, 8192, 64, splits=8192 // 64) > 0
     assert size(3, 8192, 64, splits=1) == 0
-    # 9-16 queries over >= 65536 keys: 8-query blocks of the same kernel, 512
-    # splits each (the matrix-core plan would take 256 splits of one block).
-    assert size(16, 65536, 128) >= 512 * 16 * (128 + 2) * 4
-    assert 0 < size(16, 16384, 128) < 512 * 16 * (128 + 2) * 4
+    # 9-64 queries at d = 128: the register-direct kernel, 512 key splits up
+    # to 16 queries and 256 beyond, at least min(blocks, 128), at most one
+    # split per two 16-key blocks; a request is clamped to whole blocks.
+    assert size(16, 65536, 128) == _ru(512 * 16 * 2 * 4) + _ru(512 * 16 * 128 * 4)
+    assert size(40, 65536, 128) == _ru(256 * 40 * 2 * 4) + _ru(256 * 40 * 128 * 4)
+    assert size(16, 2048, 128) == _ru(128 * 16 * 2 * 4) + _ru(128 * 16 * 128 * 4)
+    assert size(16, 2048, 128, splits=1 << 20) == size(16, 2048, 128, splits=2048 // 16)
+    # 9-16 queries over >= 65536 keys at d = 256: 8-query blocks of the
+    # few-query kernel, 512 splits each.
+    assert size(16, 65536, 256) >= 512 * 16 * (256 + 2) * 4
 
 
 def test_fastdiv_matches_division(tmp_path):
@@ -403,11 +409,12 @@ def test_attention_plan_routes_misaligned_to_generic(L):
     (the tuned kernels use 16-byte vector accesses)."""
     A = 1 << 20
     for d in (32, 64, 128, 256):
-        for M, N in ((1, 65536), (6, 4096), (64, 4096), (1024, 1024)):
+        for M, N in ((1, 65536), (6, 4096), (64, 4096), (16, 4096), (40, 65536), (1024, 1024)):
             p = kvq.AttentionParams(M, N, d, A, A, A, A, 0.0, 0)
             tuned = kvq.attention_plan(p)
-            assert tuned.kernel in (kvq.KERNEL_ATTENTION_ROWS, kvq.KERNEL_ATTENTION_MFMA)
-            assert tuned.kernel == (kvq.KERNEL_ATTENTION_ROWS if M <= 8 else kvq.KERNEL_ATTENTION_MFMA)
+            direct = 9 <= M <= 64 and ((d == 128 and (N >= 16384 or M <= 32)) or (d == 64 and N >= 32768))
+            assert tuned.kernel == (kvq.KERNEL_ATTENTION_ROWS if M <= 8 else
+                                    kvq.KERNEL_ATTENTION_DIRECT if direct else kvq.KERNEL_ATTENTION_MFMA)
             for which in range(4):
                 ptrs = [A, A, A, A]
                 ptrs[which] += 4

@@ -79,6 +79,49 @@ def test_attention_few_queries_peaked_and_splits(o, d, M, splits):
     _close(down(out), np.broadcast_to(v.astype(np.float64).mean(0), (M, d)), "flat")
 
 
+@pytest.mark.parametrize("d,M,N", [(128, M, N) for M in (9, 16, 17, 32) for N in (1, 15, 17, 4099, 65536)]
+                         + [(128, M, N) for M in (33, 64) for N in (16399, 65536)]
+                         + [(64, M, N) for M in (9, 16, 33, 64) for N in (32785, 65536)])
+def test_attention_direct_kernel(o, d, M, N):
+    """attention_direct (16 queries per wave, keys straight from memory in
+    16-key blocks) where the planner picks it -- d = 128 with up to 32
+    queries at any N or 33-64 from 16384 keys, d = 64 from 32768 keys: a
+    single key, blocks cut short by N, the plan's key splits, rows past M in
+    the last wave."""
+    rng = np.random.default_rng(M * 17 + N * 3 + d)
+    q, k, v = _problem(rng, M, N, d)
+    gq, gk, gv = up(q), up(k), up(v)
+    out = _gpu.poisoned((M, d))
+    info = kvq.attention_plan(kvq.attention_params(gq, gk, gv, out))
+    assert info.kernel == kvq.KERNEL_ATTENTION_DIRECT
+    kvq.attention_online(gq, gk, gv, out)
+    torch.cuda.synchronize()
+    _close(down(out), o.attention_f32(q, k, v), f"M={M} N={N} d={d}")
+
+
+@pytest.mark.parametrize("splits", [1, 2, 5, 1 << 20])
+@pytest.mark.parametrize("d,M,N", [(128, 12, 3000), (128, 40, 20000), (64, 40, 33000)])
+def test_attention_direct_peaked_and_splits(o, d, M, N, splits):
+    """attention_direct under any split request with large logits (frequent
+    rescales) and a NaN-filled workspace, and with identical keys (the
+    output is the mean of V)."""
+    rng = np.random.default_rng(d + splits + 100 * M)
+    q, k, v = _problem(rng, M, N, d, qscale=8.0)
+    gq, gk, gv = up(q), up(k), up(v)
+    out = _gpu.poisoned((M, d))
+    p = kvq.attention_params(gq, gk, gv, out, num_splits=splits)
+    assert kvq.attention_plan(p).kernel == kvq.KERNEL_ATTENTION_DIRECT
+    n = kvq.attention_workspace_size(p)
+    ws = torch.full((max(n, 1),), 0xFF, dtype=torch.uint8, device="cuda")
+    kvq.attention(gq, gk, gv, out, num_splits=splits, workspace=ws)
+    torch.cuda.synchronize()
+    _close(down(out), o.attention_f32(q, k, v), f"peaked, splits={splits}")
+    kf = np.repeat(rng.standard_normal((1, d)).astype(np.float32), N, axis=0)
+    out = kvq.attention_online(gq, up(kf), gv)
+    torch.cuda.synchronize()
+    _close(down(out), np.broadcast_to(v.astype(np.float64).mean(0), (M, d)), "flat")
+
+
 @pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("M,N", [(1, 1), (1, 4099), (7, 64), (128, 65), (129, 300), (200, 1000), (256, 4096),
                                  (1000, 127), (513, 2048), (63, 1024), (65, 700), (191, 256)])
