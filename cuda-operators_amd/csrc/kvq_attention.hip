@@ -315,30 +315,35 @@ __global__ __launch_bounds__(W* kWave) void attention_mfma(const AttnArgs a) {
     }
 }
 
-// attention_direct<D, W>: 9 to 32 queries (16 per wave, W waves) on the
-// same v_mfma_f32_16x16x4_f32 products as attention_mfma, but with no LDS
-// tile and no padded 64-query block: each wave streams its split's keys from
-// global memory straight into its MFMA operands, 16 keys per block, the next
-// block loading while the current one is computed.  Per block a lane loads
+// attention_direct<D, W, KW>: 9 to 64 queries (16 per wave, W query blocks)
+// on the same v_mfma_f32_16x16x4_f32 products as attention_mfma, but with no
+// LDS tile and no padded 64-query block: each wave streams keys from global
+// memory straight into its MFMA operands, 16 keys per block, the next block
+// loading while the current one is computed.  KW waves share a query block's
+// split, taking every KW-th block of it, and meet in LDS at the end (part 0
+// rescales and adds the others' (m, l, o)), so the grid has KW times the waves
+// for the same split records.  Per block a lane loads
 //   K[t + r][g * D/4 + s], s < D/4   (its A operand of S^T = K q^T), and
 //   V[t + 4 g + i][NB * r + c]        (its A operand of O^T += V^T P^T),
 // so every byte of the block is read once per wave, in 16-byte loads that
-// cover whole rows per lane group.  The W waves of a workgroup read the same
-// keys (L2 hits after the first).  Keys past the split's end read its last
+// cover whole rows per lane group.  The W query blocks of a workgroup read
+// the same keys (L2 hits after the first).  Keys past the split's end read its last
 // row (in bounds); their scores are -inf and their V values zero.  Splits
 // write the (m, l, acc) records attention_merge combines, as attention_mfma.
 constexpr int kDirectBlock = 16;  // keys per block
-template <int D, int W>
-__global__ __launch_bounds__(W* kWave) void attention_direct(const AttnArgs a) {
+template <int D, int W, int KW>
+__global__ __launch_bounds__(W* KW* kWave) void attention_direct(const AttnArgs a) {
     constexpr int DQ = D / 4;
     constexpr int NB = D / 16;
     static_assert(NB % 4 == 0, "V operand width");
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
+    const int wq = wave % W;  // query block of this wave
+    const int kw = wave / W;  // key part: blocks kw, kw + KW, ... of the split
     const int r = lane & 15;
     const int g = lane >> 4;
     const int split = blockIdx.y;
-    const int q0 = blockIdx.x * (16 * W) + wave * 16;
+    const int q0 = blockIdx.x * (16 * W) + wq * 16;
     const int k0 = split * a.chunk;
     const int k1 = min(a.N, k0 + a.chunk);
 
@@ -376,10 +381,10 @@ __global__ __launch_bounds__(W* kWave) void attention_direct(const AttnArgs a) {
     };
 
     Block cur;
-    load_block(k0, cur);
-    for (int t = k0; t < k1; t += kDirectBlock) {
+    load_block(k0 + kw * kDirectBlock, cur);
+    for (int t = k0 + kw * kDirectBlock; t < k1; t += KW * kDirectBlock) {
         Block nxt;
-        load_block(t + kDirectBlock, nxt);  // unconditional: past k1 it rereads the last row
+        load_block(t + KW * kDirectBlock, nxt);  // unconditional: past k1 it rereads the last row
         f32x4 c = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int j = 0; j < DQ / 4; j++) {
@@ -429,6 +434,36 @@ __global__ __launch_bounds__(W* kWave) void attention_direct(const AttnArgs a) {
     }
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
+    if constexpr (KW > 1) {
+        // The key parts of a query block meet in LDS: parts 1.. store their
+        // (m, l, o) lane by lane, part 0 rescales and adds them.
+        __shared__ float s_part[(KW - 1) * W][4 * NB + 2][kWave];
+        if (kw > 0) {
+            float(*const sp)[kWave] = s_part[(kw - 1) * W + wq];
+#pragma unroll
+            for (int c = 0; c < NB; c++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) sp[4 * c + i][lane] = o[c][i];
+            sp[4 * NB][lane] = m;
+            sp[4 * NB + 1][lane] = l;
+        }
+        __syncthreads();
+        if (kw > 0) return;
+#pragma unroll
+        for (int p = 0; p < KW - 1; p++) {
+            float(*const sp)[kWave] = s_part[p * W + wq];
+            const float mp = sp[4 * NB][lane];
+            const float mn = fmaxf(m, mp);
+            const float ms = mn == -INFINITY ? 0.0f : mn;
+            const float a0 = fast_exp2(m - ms), a1 = fast_exp2(mp - ms);
+            l = l * a0 + sp[4 * NB + 1][lane] * a1;
+#pragma unroll
+            for (int c = 0; c < NB; c++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) o[c][i] = o[c][i] * a0 + sp[4 * c + i][lane] * a1;
+            m = mn;
+        }
+    }
 
     const int q = q0 + r;
     if (q < a.M) {
@@ -742,10 +777,10 @@ void launch_rows_attention_d(const AttnArgs& a, int glog, hipStream_t stream) {
         default: launch_rows_attention<D, kRowsMaxQueries>(a, glog, stream); break;
     }
 }
-template <int D, int W>
+template <int D, int W, int KW>
 void launch_direct_attention(const AttnArgs& a, int glog, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((a.M + 16 * W - 1) / (16 * W)), static_cast<unsigned>(a.splits));
-    hipLaunchKernelGGL((attention_direct<D, W>), grid, dim3(W * kWave), 0, stream, a);
+    hipLaunchKernelGGL((attention_direct<D, W, KW>), grid, dim3(W * KW * kWave), 0, stream, a);
     if (a.splits > 1) {
         const dim3 mgrid(static_cast<unsigned>(
             ((static_cast<long long>(a.M) * (D / 4) << glog) + kMergeThreads - 1) / kMergeThreads));
@@ -760,9 +795,19 @@ void launch_mfma_attention_d(const AttnArgs& a, int glog, hipStream_t stream) {
     }
     if constexpr (D == 64 || D == 128) {
         if (a.direct) {
-            if (a.qblock == 16) launch_direct_attention<D, 1>(a, glog, stream);
-            else if (a.qblock == 32) launch_direct_attention<D, 2>(a, glog, stream);
-            else launch_direct_attention<D, 4>(a, glog, stream);
+            // Key parts per query block: 4, 2 or 1 (at most 8 waves).
+            if (a.qblock == 16) {
+                if (a.kparts == 4) launch_direct_attention<D, 1, 4>(a, glog, stream);
+                else if (a.kparts == 2) launch_direct_attention<D, 1, 2>(a, glog, stream);
+                else launch_direct_attention<D, 1, 1>(a, glog, stream);
+            } else if (a.qblock == 32) {
+                if (a.kparts == 4) launch_direct_attention<D, 2, 4>(a, glog, stream);
+                else if (a.kparts == 2) launch_direct_attention<D, 2, 2>(a, glog, stream);
+                else launch_direct_attention<D, 2, 1>(a, glog, stream);
+            } else {
+                if (a.kparts == 2) launch_direct_attention<D, 4, 2>(a, glog, stream);
+                else launch_direct_attention<D, 4, 1>(a, glog, stream);
+            }
             return;
         }
     }

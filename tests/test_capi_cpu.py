@@ -292,10 +292,10 @@ def test_attention_workspace_plan(L):
     assert size(8, 32, 128) == 0  # one step of 32 keys
     assert size(3, 8192, 64, splits=1 << 20) == size(3, 8192, 64, splits=8192 // 64) > 0
     assert size(3, 8192, 64, splits=1) == 0
-    # 9-64 queries at d = 128: the register-direct kernel, 512 key splits up
-    # to 16 queries and 256 beyond, at least min(blocks, 128), at most one
-    # split per two 16-key blocks; a request is clamped to whole blocks.
-    assert size(16, 65536, 128) == _ru(512 * 16 * 2 * 4) + _ru(512 * 16 * 128 * 4)
+    # 9-64 queries at d = 128: the register-direct kernel, 256 key splits, at
+    # least min(blocks, 128), at most one split per two 16-key blocks; a
+    # request is clamped to whole blocks.
+    assert size(16, 65536, 128) == _ru(256 * 16 * 2 * 4) + _ru(256 * 16 * 128 * 4)
     assert size(40, 65536, 128) == _ru(256 * 40 * 2 * 4) + _ru(256 * 40 * 128 * 4)
     assert size(16, 2048, 128) == _ru(128 * 16 * 2 * 4) + _ru(128 * 16 * 128 * 4)
     assert size(16, 2048, 128, splits=1 << 20) == size(16, 2048, 128, splits=2048 // 16)
