@@ -614,10 +614,17 @@ AttnPlan attention_plan(int M, int N, int d, bool aligned, int requested) {
     // 83.3 us in a padded matrix-core block); at d = 64 and 128 the
     // register-direct kernel below takes them.
     int qm = kvq::attention_rows_queries(M);
-    // 9-64 queries: the register-direct kernel where it beat the other
-    // kernels (one box, see the attention notes): at d = 128 from 16384 keys,
-    // or with up to 32 queries at any key count; at d = 64 from 32768 keys.
-    const bool direct_ok = M <= 64 && kvq::attention_direct_dim(d) && (d == 128 ? (N >= 16384 || M <= 32) : N >= 32768);
+    // 5-8 queries at d = 64 and 128, and 3-4 at d = 64, go to the
+    // register-direct kernel below (M = 8, N = 65536: 20.0 against 21.5 us at
+    // d = 128, 11.2 against 16.2 at d = 64; M = 4, N = 65536, d = 64: 10.8
+    // against 14.2 us); 1-4 queries at d = 128 stay here (M = 1, 2, 4: 14.0,
+    // 15.9, 17.6 us against 19.5-19.7).
+    if (kvq::attention_direct_dim(d) && (qm == kvq::kAttnRowsBlock || (d == 64 && qm == 4))) qm = 0;
+    // Up to 64 queries the register-direct kernel takes what the few-query
+    // kernel above left, where it beat the padded matrix-core block (one box):
+    // at d = 128 from 16384 keys or with up to 32 queries, at d = 64 from
+    // 32768 keys or with up to 8 queries.
+    const bool direct_ok = M <= 64 && kvq::attention_direct_dim(d) && (d == 128 ? (N >= 16384 || M <= 32) : (N >= 32768 || M <= 8));
     if (qm == 0 && M <= 2 * kvq::kAttnRowsBlock && N >= 65536 && !direct_ok) qm = kvq::kAttnRowsBlock;
     if (qm > 0) {
         // A few queries: the VALU kernel, query blocks of qm, key splits to

@@ -285,13 +285,15 @@ def test_attention_workspace_plan(L):
     assert size(128, 64, 128) == 0  # one key tile: nothing to split
     # A requested split count is clamped to whole key tiles.
     assert size(128, 8192, 64, splits=1 << 20) == size(128, 8192, 64, splits=8192 // 64) > 0
-    # Up to 8 queries: the few-query kernel splits the keys in its own steps
-    # (4096 / d keys per workgroup step): 256 splits for one query, 512 for more.
+    # Up to 4 queries at d = 128 (8 at d = 32 and 256): the few-query kernel
+    # splits the keys in its own steps (4096 / d keys per workgroup step):
+    # 256 splits for one query, 512 for more.
     assert size(1, 65536, 128) >= 256 * (128 + 2) * 4
-    assert size(8, 65536, 128) >= 512 * 8 * (128 + 2) * 4
-    assert size(8, 32, 128) == 0  # one step of 32 keys
-    assert size(3, 8192, 64, splits=1 << 20) == size(3, 8192, 64, splits=8192 // 64) > 0
-    assert size(3, 8192, 64, splits=1) == 0
+    assert size(4, 65536, 128) >= 512 * 4 * (128 + 2) * 4
+    assert size(8, 65536, 256) >= 512 * 8 * (256 + 2) * 4
+    assert size(4, 32, 128) == 0  # one step of 32 keys
+    assert size(2, 8192, 64, splits=1 << 20) == size(2, 8192, 64, splits=8192 // 64) > 0
+    assert size(2, 8192, 64, splits=1) == 0
     # 9-64 queries at d = 128: the register-direct kernel, 256 key splits, at
     # least min(blocks, 128), at most one split per two 16-key blocks; a
     # request is clamped to whole blocks.
@@ -409,11 +411,12 @@ def test_attention_plan_routes_misaligned_to_generic(L):
     (the tuned kernels use 16-byte vector accesses)."""
     A = 1 << 20
     for d in (32, 64, 128, 256):
-        for M, N in ((1, 65536), (6, 4096), (64, 4096), (16, 4096), (40, 65536), (1024, 1024)):
+        for M, N in ((1, 65536), (3, 4096), (6, 4096), (64, 4096), (16, 4096), (40, 65536), (1024, 1024)):
             p = kvq.AttentionParams(M, N, d, A, A, A, A, 0.0, 0)
             tuned = kvq.attention_plan(p)
-            direct = 9 <= M <= 64 and ((d == 128 and (N >= 16384 or M <= 32)) or (d == 64 and N >= 32768))
-            assert tuned.kernel == (kvq.KERNEL_ATTENTION_ROWS if M <= 8 else
+            rows = M <= 4 and not (d == 64 and M >= 3) if d in (64, 128) else M <= 8
+            direct = M <= 64 and ((d == 128 and (N >= 16384 or M <= 32)) or (d == 64 and (N >= 32768 or M <= 8)))
+            assert tuned.kernel == (kvq.KERNEL_ATTENTION_ROWS if rows else
                                     kvq.KERNEL_ATTENTION_DIRECT if direct else kvq.KERNEL_ATTENTION_MFMA)
             for which in range(4):
                 ptrs = [A, A, A, A]

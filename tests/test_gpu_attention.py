@@ -43,9 +43,11 @@ def _close(got, ref, what=""):
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 12, 16])
 @pytest.mark.parametrize("N", [1, 13, 4099, 65536])
 def test_attention_few_queries(o, d, M, N):
-    """Up to 8 queries (and 9-16 at N >= 65536, as 8-query blocks) run the
-    VALU kernel: key splits of whole 4096/d-key steps, a tail step past N,
-    merged records; 12 and 16 below 65536 keys take the matrix cores."""
+    """Few queries: the VALU kernel (up to 4 queries at d = 128, 2 at d = 64,
+    8 at d = 32 and 256, and 9-16 as 8-query blocks at d = 32 and 256 from
+    65536 keys) with key splits of whole 4096/d-key steps, a tail step past N
+    and merged records; the rest take attention_direct or the padded
+    matrix-core block."""
     rng = np.random.default_rng(M * 131 + N * 7 + d)
     q, k, v = _problem(rng, M, N, d)
     out = _gpu.poisoned((M, d))
@@ -58,10 +60,11 @@ def test_attention_few_queries(o, d, M, N):
 @pytest.mark.parametrize("M", [4, 6])
 @pytest.mark.parametrize("d", [64, 128, 256])
 def test_attention_few_queries_peaked_and_splits(o, d, M, splits):
-    """Large logits (frequent rescales) in the few-query kernel under any
-    split request, and identical keys (the output is the mean of V).  M = 4
-    runs the 4-query block, M = 6 the 8-query block; at d = 256 (and 128)
-    both spread a key row over d/8 lanes with 8 dims each."""
+    """Large logits (frequent rescales) under any split request, and
+    identical keys (the output is the mean of V): at d = 256 M = 4 runs the
+    few-query kernel's 4-query block and M = 6 its 8-query block (a key row
+    over d/8 lanes with 8 dims each); at d = 128 M = 4 the 4-query block; the
+    others attention_direct."""
     rng = np.random.default_rng(d + splits + 1000 * M)
     N = 3000
     q, k, v = _problem(rng, M, N, d, qscale=8.0)
@@ -79,15 +82,16 @@ def test_attention_few_queries_peaked_and_splits(o, d, M, splits):
     _close(down(out), np.broadcast_to(v.astype(np.float64).mean(0), (M, d)), "flat")
 
 
-@pytest.mark.parametrize("d,M,N", [(128, M, N) for M in (9, 16, 17, 32) for N in (1, 15, 17, 4099, 65536)]
+@pytest.mark.parametrize("d,M,N", [(128, M, N) for M in (5, 8, 9, 16, 17, 32) for N in (1, 15, 17, 4099, 65536)]
                          + [(128, M, N) for M in (33, 64) for N in (16399, 65536)]
+                         + [(64, M, N) for M in (3, 8) for N in (1, 17, 4099)]
                          + [(64, M, N) for M in (9, 16, 33, 64) for N in (32785, 65536)])
 def test_attention_direct_kernel(o, d, M, N):
     """attention_direct (16 queries per wave, keys straight from memory in
-    16-key blocks) where the planner picks it -- d = 128 with up to 32
-    queries at any N or 33-64 from 16384 keys, d = 64 from 32768 keys: a
-    single key, blocks cut short by N, the plan's key splits, rows past M in
-    the last wave."""
+    16-key blocks) where the planner picks it -- d = 128 with 5-32 queries
+    at any N or 33-64 from 16384 keys, d = 64 with 3-8 queries at any N or
+    up to 64 from 32768 keys: a single key, blocks cut short by N, the plan's
+    key splits, rows past M in the last wave."""
     rng = np.random.default_rng(M * 17 + N * 3 + d)
     q, k, v = _problem(rng, M, N, d)
     gq, gk, gv = up(q), up(k), up(v)
