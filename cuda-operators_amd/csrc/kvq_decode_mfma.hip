@@ -671,12 +671,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     if (!big) {
         len_l = lane < B ? seq_len_of(a, lane) : 0;
         n_l = (len_l + kMTile - 1) / kMTile;
-        int incl = n_l;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-            const int y = __shfl_up(incl, off);
-            if (lane >= off) incl += y;
-        }
+        const int incl = wave_inclusive_scan(n_l);
         e_l = incl - n_l;
         T = __builtin_amdgcn_readlane(incl, kWave - 1);
         wcount = B;
@@ -693,12 +688,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             lens[k] = (k < per && s0 + k < B) ? seq_len_of(a, s0 + k) : 0;
             tot += (lens[k] + kMTile - 1) / kMTile;
         }
-        int incl = tot;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-            const int y = __shfl_up(incl, off);
-            if (lane >= off) incl += y;
-        }
+        const int incl = wave_inclusive_scan(tot);
         if (lane == kWave - 1) s_wsum[wv] = incl;
         __syncthreads();
         int base = incl - tot;

@@ -40,20 +40,6 @@ constexpr int kSchedLen = 1024;  // lengths kept in LDS
 constexpr int kSchedWaves = kSchedThreads / kWave;
 constexpr int kSizeClasses = 64;
 
-// Inclusive prefix sum over the wave: Hillis-Steele steps within each
-// 16-lane row (DPP row_shr 1, 2, 4, 8; lanes shifted in from outside the row
-// add 0), then the row broadcasts of GFX9 DPP: lane 15 of rows 0 and 2 into
-// rows 1 and 3 (row_bcast:15), lane 31 into rows 2 and 3 (row_bcast:31).
-__device__ __forceinline__ int wave_inclusive_scan(int v) {
-    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
-    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
-    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
-    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
-    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
-    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
-    return v;
-}
-
 // Exclusive prefix sum of x over the workgroup (thread order); *total gets
 // the sum.  s_tmp: kSchedWaves ints of LDS, reusable after the call.
 __device__ int block_exclusive_scan(int x, int* s_tmp, int* total) {

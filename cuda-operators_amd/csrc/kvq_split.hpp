@@ -112,12 +112,7 @@ __device__ inline bool locate_fit(const DecodeArgs& a, SplitWork& w) {
     }
     const int nb = lane < B ? fit_items_for(len, chunk) : 0;
     const int cb = lane < B && len > 0 ? static_cast<int>(round_g((len + nb - 1) / nb)) : gran;
-    int incl = nb;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const int y = __shfl_up(incl, off);
-        if (lane >= off) incl += y;
-    }
+    const int incl = wave_inclusive_scan(nb);
     const int count = __builtin_amdgcn_readlane(incl, kWave - 1);
     const int U = a.Hkv * a.nsg;
     const int item = blockIdx.x / U;
