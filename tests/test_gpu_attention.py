@@ -103,6 +103,23 @@ def test_attention_direct_kernel(o, d, M, N):
     _close(down(out), o.attention_f32(q, k, v), f"M={M} N={N} d={d}")
 
 
+@pytest.mark.parametrize("d,M", [(128, 8), (128, 16), (128, 40), (64, 16)])
+def test_attention_direct_long_keys(o, d, M):
+    """attention_direct over 2^18 + 5 keys: 253 splits of 1040 keys (the
+    plan aims at 256 in whole 16-key blocks), each walked by 4 key parts (1
+    beyond 32 queries), the last split short."""
+    rng = np.random.default_rng(7 * M + d)
+    N = (1 << 18) + 5
+    q, k, v = _problem(rng, M, N, d)
+    gq, gk, gv = up(q), up(k), up(v)
+    out = _gpu.poisoned((M, d))
+    info = kvq.attention_plan(kvq.attention_params(gq, gk, gv, out))
+    assert info.kernel == kvq.KERNEL_ATTENTION_DIRECT and (info.splits, info.chunk) == (253, 1040)
+    kvq.attention_online(gq, gk, gv, out)
+    torch.cuda.synchronize()
+    _close(down(out), o.attention_f32(q, k, v), f"M={M} N={N} d={d}")
+
+
 @pytest.mark.parametrize("splits", [1, 2, 5, 1 << 20])
 @pytest.mark.parametrize("d,M,N", [(128, 12, 3000), (128, 40, 20000), (64, 40, 33000)])
 def test_attention_direct_peaked_and_splits(o, d, M, N, splits):
