@@ -204,7 +204,9 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
     //   per kv head and append, L 512-4K: 69 / 83 us).
     // * Beyond 64 the schedule's longest-first rounds balance long steps
     //   better than one static split, whose waves' rate differences add up
-    //   (cfg4: 224 us flat, 205 us scheduled; B128 L 512-2K: 66 / 62 us), so
+    //   (cfg4: 222 us flat, 203 us scheduled -- per-wave stamps: 141 tiles
+    //   per wave at 1.46-1.52 us, loop ends 10-14 us apart; B128 L 512-2K:
+    //   66 / 62 us), so
     //   the flat plan keeps only small steps, at most 16 tiles per wave for
     //   full-length sequences (B300 L 1-40: 26 / 34 us; B1000 L 0-256: 122 /
     //   125 us).
