@@ -795,19 +795,11 @@ void launch_mfma_attention_d(const AttnArgs& a, int glog, hipStream_t stream) {
     }
     if constexpr (D == 64 || D == 128) {
         if (a.direct) {
-            // Key parts per query block: 4, 2 or 1 (at most 8 waves).
-            if (a.qblock == 16) {
-                if (a.kparts == 4) launch_direct_attention<D, 1, 4>(a, glog, stream);
-                else if (a.kparts == 2) launch_direct_attention<D, 1, 2>(a, glog, stream);
-                else launch_direct_attention<D, 1, 1>(a, glog, stream);
-            } else if (a.qblock == 32) {
-                if (a.kparts == 4) launch_direct_attention<D, 2, 4>(a, glog, stream);
-                else if (a.kparts == 2) launch_direct_attention<D, 2, 2>(a, glog, stream);
-                else launch_direct_attention<D, 2, 1>(a, glog, stream);
-            } else {
-                if (a.kparts == 2) launch_direct_attention<D, 4, 2>(a, glog, stream);
-                else launch_direct_attention<D, 4, 1>(a, glog, stream);
-            }
+            // Up to 32 queries four waves share a query block's split; 33-64
+            // queries run as four query blocks of one wave each.
+            if (a.qblock == 16) launch_direct_attention<D, 1, 4>(a, glog, stream);
+            else if (a.qblock == 32) launch_direct_attention<D, 2, 4>(a, glog, stream);
+            else launch_direct_attention<D, 4, 1>(a, glog, stream);
             return;
         }
     }

@@ -575,24 +575,20 @@ DecodePlan paged_plan(const kvq_paged_decode_params* p) {
 // register file holds one per CU, below that two).
 int attention_target_workgroups(int d) { return d >= 128 ? 256 : 512; }
 
-// The register-direct attention kernel (9-64 queries, d = 64 or 128): key
-// splits per launch, KVQ_ATTN_DIRECT_SPLITS(M), but at least min(blocks, 128)
-// and at most half the 16-key blocks; KVQ_ATTN_DIRECT_KW(M) waves per query
-// block share a split.  On one box (d = 128, N = 65536): M = 16 ran 23.3 us
-// with 512 splits of one wave, 20.9 with 256 of 4 waves, 26.7 with 128 of 4,
-// 21.4 with 256 of 8; M = 32 33.9 (256 x 1) against 25.1 (256 x 4); M = 64
-// 36.8 (256 x 1) against 38.0 (256 x 2).
+// The register-direct attention kernel (up to 64 queries, d = 64 or 128):
+// key splits per launch, KVQ_ATTN_DIRECT_SPLITS(M), but at least
+// min(blocks, 128) and at most half the 16-key blocks; up to 32 queries four
+// waves per query block share a split.  On one box (d = 128, N = 65536):
+// M = 16 ran 23.3 us with 512 splits of one wave, 20.9 with 256 of 4 waves,
+// 26.7 with 128 of 4, 21.4 with 256 of 8; M = 32 33.9 (256 x 1) against 25.1
+// (256 x 4); M = 64 36.8 (256 x 1) against 38.0 (256 x 2).
 #ifndef KVQ_ATTN_DIRECT_SPLITS
 #define KVQ_ATTN_DIRECT_SPLITS(M) 256
-#endif
-#ifndef KVQ_ATTN_DIRECT_KW
-#define KVQ_ATTN_DIRECT_KW(M) ((M) <= 32 ? 4 : 1)
 #endif
 
 struct AttnPlan {
     bool tuned = false;
     bool direct = false;
-    int kparts = 1;
     int splits = 1, chunk = 0;
     int qblock = kvq::kAttnBlockWide;
     size_t ml_bytes = 0, acc_bytes = 0;
@@ -649,7 +645,6 @@ AttnPlan attention_plan(int M, int N, int d, bool aligned, int requested) {
         // 16 queries per wave; 1, 2 or 4 query blocks times the key parts per workgroup.
         p.direct = true;
         p.qblock = M <= 16 ? 16 : M <= 32 ? 32 : 64;
-        p.kparts = std::min(KVQ_ATTN_DIRECT_KW(M), p.qblock == 64 ? 2 : 4);
         const long long blocks = (static_cast<long long>(N) + 15) / 16;
         const long long cap = std::min<long long>(blocks, kvq::attention_max_splits(d));
         const long long want =
@@ -712,7 +707,6 @@ hipError_t attention_run(int M, int N, int d, const float* q, const float* k, co
     a.qblock = p.qblock;
     a.tuned = p.tuned;
     a.direct = p.direct;
-    a.kparts = p.kparts;
     a.scale_log2 = scale * 1.4426950408889634f;
     if (p.splits > 1) {
         char* base = static_cast<char*>(ws);

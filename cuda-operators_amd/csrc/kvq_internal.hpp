@@ -180,8 +180,8 @@ struct AttnArgs {
     int splits, chunk;  // key splits (grid y) and keys per split (a multiple of the key tile)
     int qblock;         // queries per workgroup: kAttnBlockWide or kAttnBlockNarrow (matrix cores),
                         // or 1, 2, 4, 8 (few-query kernel, attention_rows)
-    bool direct;        // attention_direct: qblock 16, 32 or 64 queries (16 per wave), no LDS tiles
-    int kparts;         // attention_direct: waves sharing one split's keys per query block (1, 2, 4)
+    bool direct;        // attention_direct: qblock 16, 32 or 64 queries (16 per wave), no LDS tiles;
+                        // up to 32 queries four waves share each query block's split
     float scale_log2;   // softmax scale * log2(e)
     bool tuned;         // a tuned kernel runs (tuned head dim and 16-byte aligned q, k, v, out);
                         // otherwise attention_generic, unsplit
