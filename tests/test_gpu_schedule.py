@@ -133,6 +133,25 @@ def test_schedule_at_the_one_round_limit(o, B):
     assert_close(got, want, what=f"B={B}")
 
 
+@pytest.mark.parametrize("B,G,cap", [(300, 8, 2048), (600, 8, 2048), (300, 4, 2048), (700, 1, 1024)])
+def test_schedule_several_passes(o, B, G, cap):
+    """One kv head, so one work unit per sequence: the schedule kernel (256
+    threads) walks the batch in passes of 256 sequences -- two in one round
+    (B = 300 <= 512 items), three across rounds (B = 600, and B = 700 on the
+    VALU kernel)."""
+    rng = np.random.default_rng(B + G)
+    Hkv, d = 1, 128
+    lengths = _ragged_lengths(rng, B, cap)
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, lengths=lengths)
+    info = kvq.decode_plan(kvq.decode_params(up(p["q"]), up(p["k"]), up(p["v"]), up(p["ks"]), up(p["vs"]),
+                                             torch.empty(B, Hkv * G, d, device="cuda"), lengths=up(lengths),
+                                             max_seq_len=cap))
+    assert info.split_plan == kvq.SPLITS_SCHEDULE
+    got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)[0]
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert_close(got, want, what=f"B={B} G={G}")
+
+
 @pytest.mark.parametrize("B", [63, 64, 65])
 @pytest.mark.parametrize("append", [False, True])
 def test_in_kernel_plan_limit(o, B, append):
