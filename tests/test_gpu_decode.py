@@ -69,6 +69,15 @@ def test_config_full_size(o, name):
     _check_config(o, name, 17)
 
 
+@pytest.mark.parametrize("seed", [29, 101])
+@pytest.mark.parametrize("name", ["cfg2", "cfg4"])
+def test_ragged_config_full_size_other_seeds(o, name, seed):
+    """The ragged configs at full size with the other seeds' lengths: other
+    tile-stream ranges and sequence switches for cfg2's flattened plan, other
+    schedules for cfg4."""
+    _check_config(o, name, seed)
+
+
 @pytest.mark.parametrize("splits", [1, 2, 3, 7, 16, 64, 1000])
 def test_split_counts_agree(o, splits):
     """Split + log-sum-exp merge == unsplit, for every split count (incl. more splits than tiles)."""
