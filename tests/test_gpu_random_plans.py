@@ -52,7 +52,7 @@ def _draw(rng):
     return G, d, Hkv, B, cap, lengths, splits, paged, append
 
 
-@pytest.mark.parametrize("case", range(40))
+@pytest.mark.parametrize("case", range(120))
 def test_random_plan(o, case):
     rng = np.random.default_rng(7000 + case)
     G, d, Hkv, B, cap, lengths, splits, paged, append = _draw(rng)
