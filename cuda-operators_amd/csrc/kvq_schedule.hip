@@ -60,6 +60,14 @@ __device__ int block_exclusive_scan(int x, int* s_tmp, int* total) {
     return before + v - x;
 }
 
+// Size class of a sequence's last chunk (0: a whole chunk, 63: nearly
+// empty): 64 (chunk - last) / (chunk + 1) in fp32 (no 64-bit divide), the
+// same function in both passes that use it.
+__device__ __forceinline__ int size_class(int chunk, int last) {
+    const float f = static_cast<float>(chunk - last) * (static_cast<float>(kSizeClasses) / static_cast<float>(chunk + 1));
+    return min(max(static_cast<int>(f), 0), kSizeClasses - 1);
+}
+
 __device__ __forceinline__ int clamped_len(const int32_t* lengths, int b, int max_len) {
     return min(max(lengths[b], 0), max_len);
 }
@@ -93,8 +101,18 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
         sum += len;
         if (b < kSchedLen) s_len[b] = len;
     }
+    // The wave's sum in two 32-bit halves by DPP (a lane's sum is below 2^43:
+    // at most 2^12 lengths below 2^31 each for batches up to 2^20; the
+    // halves' wave sums stay below 2^32), else by 64-bit shuffles.
+    if (B <= (1 << 20)) {
+        const unsigned lo = wave_inclusive_scan(static_cast<int>(sum & 0xFFFFF));
+        const unsigned hi = wave_inclusive_scan(static_cast<int>(sum >> 20));
+        sum = (static_cast<long long>(__builtin_amdgcn_readlane(static_cast<int>(hi), kWave - 1)) << 20) +
+              static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(lo), kWave - 1));
+    } else {
 #pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+        for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    }
     if (lane == 0) s_sum[wave] = sum;
     if (t < kSizeClasses) s_class[t] = 0;
     if (t == 0) s_best = INT_MAX;
@@ -172,7 +190,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
                 if (pos < items_cap) put_item(items, pos, b, s, n, rec_carry + pre_n, chunk, len);
             }
             const int last = len - (n - 1) * chunk;  // in [0, chunk]
-            const int cls = static_cast<int>(static_cast<long long>(chunk - last) * kSizeClasses / (chunk + 1));
+            const int cls = size_class(chunk, last);
             atomicAdd(&s_class[cls], 1);
         }
         rec_carry += tot_n;
@@ -189,7 +207,7 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
         const int len = len_of(b);
         const int n = len == 0 ? 1 : (len + chunk - 1) / chunk;
         const int last = len - (n - 1) * chunk;
-        const int cls = static_cast<int>(static_cast<long long>(chunk - last) * kSizeClasses / (chunk + 1));
+        const int cls = size_class(chunk, last);
         const int pos = atomicAdd(&s_class[cls], 1);
         if (pos < items_cap) put_item(items, pos, b, n - 1, n, seq[b].x, chunk, len);
     }
