@@ -395,11 +395,75 @@ __device__ inline void merge_flat(const DecodeArgs& a, const RecMap& map, size_t
     }
 }
 
+// Merge of 17 to 2 * kFlatSplits splits in one round trip: two adjacent
+// lanes per (head, 16-byte output column), lane half j taking splits j,
+// j + 2, ...; the pair exchanges its maxima, then its sums and accumulators,
+// with lane shuffles (no LDS, no barrier), as merge_flat does for one lane.
+__device__ inline void merge_flat_pairs(const DecodeArgs& a, const RecMap& map, size_t bhq0, int nheads,
+                                        int nsplit) {
+    const int d = a.d;
+    const int cpr = d >> 2;
+    const unsigned span = static_cast<unsigned>(merge_span(map, nheads, nsplit));
+    const buf_rsrc mlr = make_rsrc(a.part_ml + map.r0 * 2, span * 8u);
+    const buf_rsrc accr = make_rsrc(a.part_acc + map.r0 * d, span * static_cast<unsigned>(d) * 4u);
+    typedef int v2i_t __attribute__((ext_vector_type(2)));
+    const int half = threadIdx.x & 1;
+    // Every lane of a wave runs the same number of iterations (blockDim is a
+    // multiple of 64), so the shuffles below always have their partner.
+    for (int c0 = threadIdx.x >> 1; c0 < ((nheads * cpr + kWave / 2 - 1) / (kWave / 2)) * (kWave / 2);
+         c0 += blockDim.x >> 1) {
+        const bool live = c0 < nheads * cpr;
+        const int c = live ? c0 : 0;
+        const int h = c / cpr;
+        const int col = c - h * cpr;
+        v2i_t ml[kFlatSplits];
+        v4i_t acc[kFlatSplits];
+#pragma unroll
+        for (int k = 0; k < kFlatSplits; k++) {
+            const int sp = 2 * k + half;
+            const int rec = h * map.hs + sp * map.ss;
+            if (sp < nsplit) {
+                ml[k] = __builtin_amdgcn_raw_buffer_load_b64(mlr, rec * 8, 0, kCoherent);
+                acc[k] = __builtin_amdgcn_raw_buffer_load_b128(accr, (rec * d + 4 * col) * 4, 0, kCoherent);
+            }
+        }
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < kFlatSplits; k++)
+            if (2 * k + half < nsplit) M = fmaxf(M, __int_as_float(ml[k].x));
+        M = fmaxf(M, __shfl_xor(M, 1));
+        const float Ms = M == -INFINITY ? 0.0f : M;
+        float L = 0.0f;
+        float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int k = 0; k < kFlatSplits; k++) {
+            if (2 * k + half < nsplit) {
+                const float w = fast_exp2(__int_as_float(ml[k].x) - Ms);
+                L = fmaf(__int_as_float(ml[k].y), w, L);
+                A.x = fmaf(__int_as_float(acc[k].x), w, A.x);
+                A.y = fmaf(__int_as_float(acc[k].y), w, A.y);
+                A.z = fmaf(__int_as_float(acc[k].z), w, A.z);
+                A.w = fmaf(__int_as_float(acc[k].w), w, A.w);
+            }
+        }
+        L += __shfl_xor(L, 1);
+        A.x += __shfl_xor(A.x, 1);
+        A.y += __shfl_xor(A.y, 1);
+        A.z += __shfl_xor(A.z, 1);
+        A.w += __shfl_xor(A.w, 1);
+        if (live && half == 0) {
+            float* o = a.out + (bhq0 + h) * d + 4 * col;
+            o[0] = A.x / L, o[1] = A.y / L, o[2] = A.z / L, o[3] = A.w / L;
+        }
+    }
+}
+
 // Called by every thread of a workgroup after its store_result calls: counts
 // the split's arrival and, in the last workgroup of the work unit, merges the
 // records of rows [bhq0, bhq0 + nheads).  s_last: one int of LDS.  FLAT: up
-// to kFlatSplits splits merge with merge_flat (its registers are not worth
-// taking from the FMA kernel, whose ragged batches rarely split).
+// to kFlatSplits splits merge with merge_flat, up to twice that with
+// merge_flat_pairs (their registers are not worth taking from the FMA
+// kernel, whose ragged batches rarely split).
 template <bool FLAT = false>
 __device__ __forceinline__ void finish_split(const DecodeArgs& a, int unit, const RecMap& map, size_t bhq0,
                                              int nheads, int nsplit, int* s_last) {
@@ -414,6 +478,8 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, int unit, cons
     if (*s_last) {
         if (FLAT && nsplit <= kFlatSplits && merge_group_fits(a, map, nheads, nsplit)) {
             merge_flat(a, map, bhq0, nheads, nsplit);
+        } else if (FLAT && nsplit <= 2 * kFlatSplits && merge_group_fits(a, map, nheads, nsplit)) {
+            merge_flat_pairs(a, map, bhq0, nheads, nsplit);
         } else if (merge_group_fits(a, map, nheads, nsplit)) {
             merge_group(a, map, bhq0, nheads, nsplit);
         } else {

@@ -89,6 +89,23 @@ def test_split_counts_agree(o, splits):
     assert_close(got, want, what=f"splits={splits}")
 
 
+@pytest.mark.parametrize("splits,L", [(17, 2100), (24, 3000), (31, 3900), (32, 4000)])
+def test_merge_of_17_to_32_splits(o, splits, L):
+    """17..32 splits: the last split's workgroup merges with two lanes per output
+    column (splits of one parity each), every sequence length split differently."""
+    rng = np.random.default_rng(splits + L)
+    lengths = np.array([L, 1, L - 1, (2 * L) // 5], np.int32)
+    p = make_problem(rng, 4, 8, 2, L, 128, o.quantize_rows, dist="outlier", lengths=lengths)
+    prm = kvq.DecodeParams(batch=4, num_q_heads=8, num_kv_heads=2, head_dim=128, capacity=L, max_seq_len=L,
+                           lengths=4096, q=4096, k_cache=4096, v_cache=4096, k_scale=4096, v_scale=4096,
+                           out=4096, num_splits=splits)
+    info = kvq.decode_plan(prm)
+    assert (info.kernel, info.splits) == (kvq.KERNEL_DECODE_MFMA, splits)
+    got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths, splits=splits)[0]
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert_close(got, want, what=f"splits={splits} L={L}")
+
+
 @pytest.mark.parametrize("G", [1, 2, 3, 4, 6, 8, 12, 16])
 @pytest.mark.parametrize("d", [64, 128])
 def test_group_sizes(o, G, d):
