@@ -115,6 +115,14 @@ bool flat_enabled() {
     return on;
 }
 
+// KVQ_SCHEDULE_LAUNCH=1 keeps the separate schedule launch for the ragged
+// matrix-core batches whose schedule the decode kernel derives itself
+// (locate_lpt), for comparison.
+bool lpt_enabled() {
+    static const bool on = !env_on("KVQ_SCHEDULE_LAUNCH");
+    return on;
+}
+
 unsigned prefill_max_groups() {
     static const unsigned g = [] {
         const char* s = getenv("KVQ_PREFILL_MAX_GROUPS");
@@ -256,13 +264,25 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
         p.sched_items = B + (p.sched_target + U - 1) / U + 1;
         p.splits = 0;
         p.chunk = 0;
+        // Beyond one round of items (B > target / U), up to kLptMaxSeqs
+        // sequences and a few rounds of B items, the matrix-core kernel
+        // derives the schedule itself (locate_lpt): one launch per step
+        // instead of two (one box: cfg4 200.9 against 202.9-203.3 us; B128
+        // Hq32/Hkv8 L 512-2K 61.3 / 63.0 us; B512 Hq64/Hkv8 L 256-2K 230.5 /
+        // 232.6 us; B300 Hq64/Hkv8 L 1-8K 404.8 / 408.2 us).
+        p.lpt = p.kernel == kvq::Kernel::Mfma && B > p.sched_target / U && B <= kvq::kLptMaxSeqs &&
+                static_cast<long>(B) * U <=
+                    static_cast<long>(max_len >= kvq::kLptLongTokens ? kvq::kLptMaxRounds : kvq::kLptMaxRounds / 2) *
+                        p.sched_target &&
+                (gran & (gran - 1)) == 0 && p.sched_target < (1 << 23) && max_len <= (1 << 30) && lpt_enabled();
         const size_t recs = static_cast<size_t>(p.sched_items) * Hq;
         p.counter_bytes = kCounterBytes;
         p.sched_bytes =
-            round_up((kvq::kSchedHeader + kvq::kSchedItemInts * static_cast<size_t>(p.sched_items) +
-                      2 * static_cast<size_t>(B)) *
-                         sizeof(int),
-                     kAlign);
+            p.lpt ? 0
+                  : round_up((kvq::kSchedHeader + kvq::kSchedItemInts * static_cast<size_t>(p.sched_items) +
+                              2 * static_cast<size_t>(B)) *
+                                 sizeof(int),
+                             kAlign);
         p.ml_bytes = round_up(recs * 2 * sizeof(float), kAlign);
         p.acc_bytes = round_up(recs * static_cast<size_t>(d) * sizeof(float), kAlign);
         return p;
@@ -311,7 +331,8 @@ size_t plan_bytes(const DecodePlan& p) { return p.counter_bytes + p.sched_bytes 
 void bind_workspace(DecodeArgs& a, const DecodePlan& p, void* ws) {
     char* base = static_cast<char*>(ws);
     a.counters = p.counters ? reinterpret_cast<int*>(base) : nullptr;
-    a.sched = p.scheduled ? reinterpret_cast<const int*>(base + p.counter_bytes) : nullptr;
+    a.sched = p.scheduled && !p.lpt ? reinterpret_cast<const int*>(base + p.counter_bytes) : nullptr;
+    a.lpt_target = p.lpt ? p.sched_target : 0;
     a.sched_items = p.sched_items;
     a.fit_items = p.fit ? p.sched_items : 0;
     a.flat = p.flat ? 1 : 0;
@@ -423,10 +444,10 @@ kvq_plan_info decode_info(const DecodePlan& p) {
                : p.kernel == kvq::Kernel::Valu ? KVQ_KERNEL_DECODE_VALU
                                                : KVQ_KERNEL_DECODE_GENERIC;
     r.heads_per_group = p.sg;
-    r.split_plan = p.flat        ? KVQ_SPLITS_TILES
-                   : p.fit       ? KVQ_SPLITS_IN_KERNEL
-                   : p.scheduled ? KVQ_SPLITS_SCHEDULE
-                                 : KVQ_SPLITS_STATIC;
+    r.split_plan = p.flat           ? KVQ_SPLITS_TILES
+                   : p.fit || p.lpt ? KVQ_SPLITS_IN_KERNEL
+                   : p.scheduled    ? KVQ_SPLITS_SCHEDULE
+                                    : KVQ_SPLITS_STATIC;
     r.splits = r.split_plan == KVQ_SPLITS_STATIC ? p.splits : 0;
     r.chunk = r.split_plan == KVQ_SPLITS_STATIC ? p.chunk : 0;
     r.query_block = 0;

@@ -553,7 +553,7 @@ long decode_grid(const DecodeArgs& a, const DecodePlan& p) {
 
 hipError_t launch_decode(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
     hipError_t err;
-    if (p.scheduled) {
+    if (p.scheduled && !p.lpt) {
         err = launch_schedule(a.lengths, a.B, a.max_len, a.Hkv * p.nsg, p.sched_target, p.sched_gran,
                               p.sched_items, const_cast<int*>(a.sched), stream);
         if (err != hipSuccess) return err;

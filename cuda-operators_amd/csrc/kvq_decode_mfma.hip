@@ -105,16 +105,20 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // V tile buffers during the tile loop; the waves' results afterwards
     // (rows padded by one float, so the lanes of one result column, 16 rows
     // apart, hit different banks).
+    // (Before the tile loop, the in-kernel schedule's scratch.)
     union TileOrResult {
         int8_t v[kMWaves][2][kMTile * D];
         float acc[kMWaves][16][D + 1];
+        LptScratch lpt;
     };
+    static_assert(kMWaves * kWave == kLptThreads, "locate_lpt's workgroup size");
     __shared__ __align__(16) TileOrResult s_u;
     auto& s_v = s_u.v;
     auto& s_acc = s_u.acc;
     __shared__ float s_ml[kMWaves][G][2];
     __shared__ __align__(16) int8_t s_newq[2][D];
     __shared__ int s_last;
+    __shared__ int s_pick[5];
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -124,6 +128,8 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     SplitWork w;
     if constexpr (FIT) {
         if (!locate_fit(a, w)) return;
+    } else if (a.lpt_target > 0) {
+        if (!locate_lpt(a, w, s_u.lpt, s_pick)) return;
     } else {
         if (!locate_work(a, w)) return;
     }

@@ -74,6 +74,28 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
     return v;
 }
 
+// Inclusive prefix max over the wave of non-negative ints (the steps of
+// wave_inclusive_scan with max; lanes shifted in from outside a row give 0).
+__device__ __forceinline__ int wave_inclusive_max_nonneg(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false));
+    return v;
+}
+
+// Size class of a sequence's last chunk under a split schedule (0: a whole
+// chunk, kClasses - 1: nearly empty): kClasses (chunk - last) / (chunk + 1)
+// in fp32 (no 64-bit divide).  Longest-first order dispatches class 0 first.
+template <int kClasses>
+__device__ __forceinline__ int last_chunk_class(int chunk, int last) {
+    const float f =
+        static_cast<float>(chunk - last) * (static_cast<float>(kClasses) / static_cast<float>(chunk + 1));
+    return min(max(static_cast<int>(f), 0), kClasses - 1);
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);

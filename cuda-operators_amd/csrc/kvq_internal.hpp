@@ -56,6 +56,8 @@ struct DecodeArgs {
     int splits;              // grid splits per sequence (static splits)
     int chunk;               // tokens per split (static splits)
     int nsg;                 // head groups per kv head (G / heads per workgroup)
+    int lpt_target;          // > 0: the matrix-core kernel derives the split schedule itself (locate_lpt)
+                             // for this many workgroups per round (the schedule kernel's target)
     float scale_log2;        // softmax_scale * log2(e)
 };
 
@@ -91,6 +93,18 @@ constexpr int kFlatMaxSeqs = 4096;
 #define KVQ_FLAT_SWITCH_TILES 2
 #endif
 constexpr int kFlatSwitchTiles = KVQ_FLAT_SWITCH_TILES;
+// Most sequences of a ragged batch whose multi-round split schedule the
+// matrix-core kernel derives itself (locate_lpt) instead of reading it from a
+// schedule launch: two per thread of its 256.  Every workgroup pays for the
+// derivation at its start, so larger batches (B1024 Hq32/Hkv8 L 64-1K: 257
+// against 245 us) and many rounds of short items keep the launch: at most
+// kLptMaxRounds rounds of B items, half that below kLptLongTokens tokens of
+// capacity (B512 Hq32/Hkv8 L 64-1K, 8 rounds: 124.9 against 123.1 us).
+constexpr int kLptMaxSeqs = 512;
+constexpr int kLptMaxRounds = 8;
+constexpr int kLptLongTokens = 2048;
+// Size classes of a sequence's last chunk in the longest-first order.
+constexpr int kSizeClasses = 64;
 
 // Which decode kernel a plan runs.
 enum class Kernel {
@@ -111,6 +125,7 @@ struct DecodePlan {
     bool scheduled;  // ragged batch: the split schedule is computed on the device
     bool fit;        // ragged batch planned inside the matrix-core kernel (one round, no schedule launch)
     bool flat;       // with fit: the flattened tile-stream plan (decode_mfma_flat)
+    bool lpt;        // with scheduled: the matrix-core kernel derives the schedule (no schedule launch)
     int sched_items;     // schedule item capacity (scheduled)
     int sched_target;    // workgroups the schedule aims for (scheduled)
     int sched_gran;      // chunk granularity in tokens (scheduled)

@@ -38,7 +38,6 @@ namespace {
 constexpr int kSchedThreads = 256;
 constexpr int kSchedLen = 1024;  // lengths kept in LDS
 constexpr int kSchedWaves = kSchedThreads / kWave;
-constexpr int kSizeClasses = 64;
 
 // Exclusive prefix sum of x over the workgroup (thread order); *total gets
 // the sum.  s_tmp: kSchedWaves ints of LDS, reusable after the call.
@@ -60,13 +59,8 @@ __device__ int block_exclusive_scan(int x, int* s_tmp, int* total) {
     return before + v - x;
 }
 
-// Size class of a sequence's last chunk (0: a whole chunk, 63: nearly
-// empty): 64 (chunk - last) / (chunk + 1) in fp32 (no 64-bit divide), the
-// same function in both passes that use it.
-__device__ __forceinline__ int size_class(int chunk, int last) {
-    const float f = static_cast<float>(chunk - last) * (static_cast<float>(kSizeClasses) / static_cast<float>(chunk + 1));
-    return min(max(static_cast<int>(f), 0), kSizeClasses - 1);
-}
+// The same class function in both passes that use it.
+__device__ __forceinline__ int size_class(int chunk, int last) { return last_chunk_class<kSizeClasses>(chunk, last); }
 
 __device__ __forceinline__ int clamped_len(const int32_t* lengths, int b, int max_len) {
     return min(max(lengths[b], 0), max_len);
@@ -123,7 +117,9 @@ __global__ __launch_bounds__(kSchedThreads) void schedule_kernel(const int32_t* 
 
     int* items = sched + kSchedHeader;
     int2* seq = reinterpret_cast<int2*>(items + kSchedItemInts * items_cap);  // (rec_base, chunk) per sequence
-    const long long cmax = (static_cast<long long>(max(max_len, 1)) + gran - 1) / gran * gran;
+    // (At most INT_MAX rounded down to the granularity: a chunk is an int.)
+    const long long cmax = min((static_cast<long long>(max(max_len, 1)) + gran - 1) / gran * gran,
+                               static_cast<long long>(INT_MAX) / gran * gran);
     const int S = target / units;
 
     if (B <= S && B <= kSchedLen) {

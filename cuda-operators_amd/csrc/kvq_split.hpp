@@ -131,6 +131,215 @@ __device__ inline bool locate_fit(const DecodeArgs& a, SplitWork& w) {
     return true;
 }
 
+// In-kernel longest-first schedule (a.lpt_target > 0): a ragged batch of
+// S < B <= kLptMaxSeqs sequences, S = a.lpt_target / U items per round.
+// Every workgroup derives the multi-round schedule of schedule_kernel from the
+// lengths and takes its own item, so the decode step needs no schedule
+// launch:
+// * chunk = the tokens of all sequences times U over the target, rounded up
+//   to the granularity, at most the longest possible sequence;
+// * items: the whole chunks of every sequence first (sequence order, split
+//   order), then each sequence's last chunk, longest first (kSizeClasses
+//   size classes, sequence order within a class) -- list scheduling in
+//   longest-processing-time order; split s of sequence b covers tokens
+//   [s * chunk, (s + 1) * chunk), its first record is the splits of the
+//   sequences before b.
+// When no sequence is longer than the chunk (every sequence one item) the
+// workgroup orders the sequences by their whole lengths, counted while the
+// chunk is still being summed, and skips the scans of whole chunks and
+// records.  Two sequences per thread (b = 2t + k) of a 256-thread
+// workgroup; scratch in LDS that the kernel reuses after the call (no read of
+// it follows the last barrier), and pick: 5 ints of LDS that stay.
+constexpr int kLptThreads = 256;
+constexpr int kLptPerThread = kLptMaxSeqs / kLptThreads;
+constexpr int kLptWaves = kLptThreads / kWave;
+constexpr int kLptGroups = kLptMaxSeqs / kWave;
+struct LptScratch {
+    unsigned long long bits[kSizeClasses][kLptGroups];  // sequences 64 g + i whose last chunk has class c
+    int len[kLptMaxSeqs];
+    int rec[kLptMaxSeqs];  // first record of each sequence (when some sequence splits)
+    int hist[kSizeClasses];
+    int red[5][kLptWaves];  // per wave: length sum (low 20 bits, the rest), max; splits, whole chunks
+};
+
+// Lowest set lane of a wave mask, 0 for an empty mask (index clamp).
+__device__ __forceinline__ int first_lane(unsigned long long m) { return m ? __builtin_ctzll(m) : 0; }
+
+// Sequence b of the j-th last chunk in longest-first order (wave 0; j below
+// the class counts' sum, B, so every mask below has a lane; the clamps only
+// keep indices in range).
+__device__ __forceinline__ int lpt_select(const LptScratch& s, int j, int lane, int B) {
+    const int c = s.hist[lane];
+    const int incl = wave_inclusive_scan(c);
+    const int cls = first_lane(__builtin_amdgcn_ballot_w64(incl > j));
+    j -= __builtin_amdgcn_readlane(incl - c, cls);
+    const int p = lane < kLptGroups ? __builtin_popcountll(s.bits[cls][lane]) : 0;
+    const int incl2 = wave_inclusive_scan(p);
+    const int grp = min(first_lane(__builtin_amdgcn_ballot_w64(incl2 > j)), kLptGroups - 1);
+    j -= __builtin_amdgcn_readlane(incl2 - p, grp);
+    const unsigned long long word = s.bits[cls][grp];
+    const bool hit = ((word >> lane) & 1ull) && __builtin_popcountll(word & ((1ull << lane) - 1ull)) == j;
+    return min(grp * kWave + first_lane(__builtin_amdgcn_ballot_w64(hit)), B - 1);
+}
+
+__device__ inline bool locate_lpt(const DecodeArgs& a, SplitWork& w, LptScratch& s, int* pick) {
+    const int U = a.Hkv * a.nsg;
+    const int item = blockIdx.x / U;
+    const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int wave = t / kWave;
+    const int B = a.B;
+    const int gran = a.fit_gran;
+    // The device lengths (never null under this plan), loaded unconditionally
+    // at in-bounds indices so that the loads are in flight together,
+    // while the class counts are cleared.
+    int len[kLptPerThread];
+#pragma unroll
+    for (int k = 0; k < kLptPerThread; k++) len[k] = a.lengths[min(kLptPerThread * t + k, B - 1)];
+    auto clear_classes = [&]() {
+        unsigned long long* const bits = &s.bits[0][0];
+#pragma unroll
+        for (int i = 0; i < kSizeClasses * kLptGroups / kLptThreads; i++) bits[t + i * kLptThreads] = 0ull;
+        if (t < kSizeClasses) s.hist[t] = 0;
+    };
+    auto add_class = [&](int b, int c) {
+        atomicAdd(&s.hist[c], 1);
+        atomicOr(&s.bits[c][b / kWave], 1ull << (b % kWave));
+    };
+    clear_classes();
+    __syncthreads();
+    // The classes as whole sequences (chunk = cmax), which order the items
+    // longest first whenever no sequence splits, whatever the chunk.
+    const unsigned gm = static_cast<unsigned>(gran) - 1u;
+    const int cmax = static_cast<int>((static_cast<unsigned>(max(a.max_len, 1)) + gm) & ~gm);
+    long long sum = 0;
+    int mx = 0;
+#pragma unroll
+    for (int k = 0; k < kLptPerThread; k++) {
+        const int b = kLptPerThread * t + k;
+        len[k] = b < B ? min(max(len[k], 0), a.max_len) : 0;
+        sum += len[k];
+        mx = max(mx, len[k]);
+        if (b < B) {
+            s.len[b] = len[k];
+            add_class(b, last_chunk_class<kSizeClasses>(cmax, len[k]));
+        }
+    }
+    // Lane sums are below 2^32: the wave sums of their low 20 bits and of the
+    // rest stay below 2^26 and 2^18.
+    const int lo = wave_inclusive_scan(static_cast<int>(sum & 0xFFFFF));
+    const int hi = wave_inclusive_scan(static_cast<int>(sum >> 20));
+    const int wm = wave_inclusive_max_nonneg(mx);
+    if (lane == kWave - 1) {
+        s.red[0][wave] = lo;
+        s.red[1][wave] = hi;
+        s.red[2][wave] = wm;
+    }
+    __syncthreads();
+    long long total = 0;
+    int longest = 0;
+#pragma unroll
+    for (int v = 0; v < kLptWaves; v++) {
+        total += (static_cast<long long>(s.red[1][v]) << 20) + s.red[0][v];
+        longest = max(longest, s.red[2][v]);
+    }
+    // chunk = min(cmax, max(gran, round_up(ceil(total * U / target), gran)))
+    // without 64-bit divides (gran is a power of two): below target * cmax
+    // the numerator is under 2^53 and the target under 2^23, so the double
+    // quotient is never rounded across an integer.
+    const long long num = total * U;
+    int chunk = cmax;
+    if (num < static_cast<long long>(a.lpt_target) * cmax) {
+        const int want = static_cast<int>(ceil(static_cast<double>(num) / static_cast<double>(a.lpt_target)));
+        chunk = min(cmax, max(gran, static_cast<int>((static_cast<unsigned>(want) + gm) & ~gm)));
+    }
+
+    if (longest <= chunk) {
+        // Every sequence is one item: item j is the j-th longest.
+        if (item >= B) return false;
+        if (wave == 0) {
+            const int b = lpt_select(s, item, lane, B);
+            if (lane == 0) {
+                pick[0] = b;
+                pick[1] = 0;
+                pick[2] = 1;
+                pick[3] = b;
+                pick[4] = s.len[b];
+            }
+        }
+    } else {
+        // Some sequence splits: the classes of the last chunks replace those
+        // of the whole sequences.
+        clear_classes();
+        __syncthreads();
+        int n[kLptPerThread], full[kLptPerThread];
+        int nt = 0, ft = 0;
+#pragma unroll
+        for (int k = 0; k < kLptPerThread; k++) {
+            const int b = kLptPerThread * t + k;
+            n[k] = b < B ? (len[k] == 0 ? 1 : (len[k] + chunk - 1) / chunk) : 0;
+            full[k] = b < B ? n[k] - 1 : 0;
+            if (b < B) add_class(b, last_chunk_class<kSizeClasses>(chunk, len[k] - full[k] * chunk));
+            nt += n[k];
+            ft += full[k];
+        }
+        const int in = wave_inclusive_scan(nt);
+        const int inf = wave_inclusive_scan(ft);
+        if (lane == kWave - 1) {
+            s.red[3][wave] = in;
+            s.red[4][wave] = inf;
+        }
+        __syncthreads();
+        int r = in - nt, f = inf - ft, whole = 0;
+#pragma unroll
+        for (int v = 0; v < kLptWaves; v++) {
+            r += v < wave ? s.red[3][v] : 0;
+            f += v < wave ? s.red[4][v] : 0;
+            whole += s.red[4][v];
+        }
+        if (item >= whole + B) return false;
+#pragma unroll
+        for (int k = 0; k < kLptPerThread; k++) {
+            const int b = kLptPerThread * t + k;
+            if (b < B) {
+                s.rec[b] = r;
+                if (item >= f && item < f + full[k]) {
+                    pick[0] = b;
+                    pick[1] = item - f;
+                    pick[2] = n[k];
+                    pick[3] = r;
+                    pick[4] = len[k];
+                }
+            }
+            r += n[k];
+            f += full[k];
+        }
+        __syncthreads();
+        if (item >= whole && wave == 0) {
+            const int b = lpt_select(s, item - whole, lane, B);
+            if (lane == 0) {
+                const int lb = s.len[b];
+                const int nb = lb == 0 ? 1 : (lb + chunk - 1) / chunk;
+                pick[0] = b;
+                pick[1] = nb - 1;
+                pick[2] = nb;
+                pick[3] = s.rec[b];
+                pick[4] = lb;
+            }
+        }
+    }
+    __syncthreads();
+    w.b = pick[0];
+    w.split = pick[1];
+    w.nsplit = pick[2];
+    w.rec = pick[3];
+    w.len = pick[4];
+    w.unit = w.b * U + (blockIdx.x - item * U);
+    w.t0 = w.split * chunk;
+    w.t1 = min(w.len, w.t0 + chunk);
+    return true;
+}
+
 // Partial record of row bhq0 + h, split s: r0 + h * hs + s * ss (records of
 // 2 floats in part_ml, d floats in part_acc).
 struct RecMap {
@@ -143,11 +352,12 @@ __device__ __forceinline__ RecMap rec_map_static(const DecodeArgs& a, size_t bhq
     return {bhq0 * a.splits, a.splits, 1};
 }
 
-// Records of workgroup w's sequence: under the in-kernel plan (locate_fit) or
-// the split schedule, split s of sequence b owns records (w.rec + s) * Hq + hq;
+// Records of workgroup w's sequence: under the in-kernel plans (locate_fit,
+// locate_lpt) or the split schedule, split s of sequence b owns records
+// (w.rec + s) * Hq + hq;
 // otherwise static splits.
 __device__ __forceinline__ RecMap rec_map(const DecodeArgs& a, const SplitWork& w, size_t bhq0) {
-    if (a.fit_items > 0 || a.sched)
+    if (a.fit_items > 0 || a.sched || a.lpt_target > 0)
         return {static_cast<size_t>(w.rec) * a.Hq + (bhq0 - static_cast<size_t>(w.b) * a.Hq), 1, a.Hq};
     return rec_map_static(a, bhq0);
 }

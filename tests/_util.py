@@ -141,3 +141,33 @@ def make_problem(rng, B, Hq, Hkv, cap, d, quantize, dist="normal", lengths=None)
     k, ks = quantize(kf)
     v, vs = quantize(vf)
     return dict(q=q, k=k, v=v, ks=ks, vs=vs, lengths=lengths)
+
+
+# ---------------------------------------------------------------------------
+# ragged batches for the matrix-core kernel's in-kernel split schedule
+# ---------------------------------------------------------------------------
+LPT_CASES = {
+    # B, Hq, Hkv, d, cap: 8 work units per sequence, so more than 512 / 8 = 64
+    # sequences take longest-first rounds.  "whole": lengths in [cap/2, cap],
+    # every sequence one item; "split": one sequence of cap tokens among short
+    # ones (and an empty one), cut into many chunks.
+    "whole": (100, 32, 8, 64, 1024),
+    "split": (80, 64, 4, 64, 4096),
+    "cfg4_shape": (65, 64, 8, 128, 1024),
+}
+
+
+def lpt_case(name, quantize):
+    """Seeded problem (dict of make_problem plus k_new / v_new) for LPT_CASES[name]."""
+    B, Hq, Hkv, d, cap = LPT_CASES[name]
+    rng = np.random.default_rng(sum(map(ord, name)))
+    if name == "split":
+        lengths = rng.integers(1, 100, B).astype(np.int32)
+        lengths[:3] = [cap, 0, 1]
+    else:
+        lengths = rng.integers(cap // 2, cap + 1, B).astype(np.int32)
+        lengths[:2] = [cap, cap // 2]
+    p = make_problem(rng, B, Hq, Hkv, cap, d, quantize, dist="student_t", lengths=lengths)
+    p["k_new"] = student_t4(rng, (B, Hkv, d))
+    p["v_new"] = student_t4(rng, (B, Hkv, d))
+    return p

@@ -131,7 +131,7 @@ kvq_decode_params decode_params(int B, int Hq, int Hkv, int d, int cap, int max_
 }
 
 void decode_plans() {
-    const int batches[] = {1, 2, 3, 7, 16, 63, 64, 65, 256, 1000, 4096, 4097, 65536};
+    const int batches[] = {1, 2, 3, 7, 16, 63, 64, 65, 256, 512, 513, 1000, 1024, 1025, 4096, 4097, 65536};
     const int groups[][2] = {{1, 1}, {8, 8}, {32, 32}, {32, 8}, {64, 8}, {32, 2}, {16, 1}, {12, 3}, {5, 5}, {128, 1}};
     const int dims[] = {1, 3, 32, 64, 96, 128, 256, 512, 1024};
     const int lens[] = {1, 31, 32, 33, 1000, 4096, 1 << 17, 1 << 24, INT_MAX};

@@ -12,6 +12,7 @@ import importlib
 import os
 import re
 import subprocess
+import sys
 
 import pytest
 
@@ -145,18 +146,22 @@ def _ru(x, a=256):
     return (x + a - 1) // a * a
 
 
-@pytest.mark.parametrize("B", [8, 24, 31, 32, 64, 65, 512, 513, 1025])
-def test_matrix_core_plan_by_workspace(L, B):
+@pytest.mark.parametrize("B,cap", [(8, 512), (24, 512), (31, 512), (32, 512), (64, 512), (65, 512), (512, 512),
+                                   (513, 512), (1025, 512), (100, 8192), (256, 8192), (257, 8192), (512, 8192),
+                                   (513, 8192)])
+def test_matrix_core_plan_by_workspace(L, B, cap):
     """Grouped-query heads at d = 128 (matrix-core kernel, 4 heads per
     workgroup, U = Hkv work units per sequence), ragged lengths: the kernel
     plans the batch itself with S = 256 / U workgroups per work unit -- the
     flattened tile plan (records for 4 S waves + B ids) when B >= S / 4 and
     either B <= 64 or the batch has at most 16 tiles of 32 tokens per wave at
     full length; below S / 4 sequences whole items per sequence (S items of
-    records); otherwise the device split schedule, whose words come on top of
-    its own B + 512 / U + 1 items of records.  Records hold (d + 2) floats
-    per query head after the counter block."""
-    Hq, Hkv, d, cap = 8, 2, 128, 512
+    records); otherwise the device split schedule for 512 workgroups, with
+    B + 512 / U + 1 items of records: derived inside the decode kernel beyond
+    one round of items (B > 512 / U) up to 512 sequences and 8 rounds
+    (B * U <= 8 * 512; 4 below 2048 tokens of capacity), else written by a
+    schedule launch whose words come on top.  Records hold (d + 2) floats per query head after the counter block."""
+    Hq, Hkv, d = 8, 2, 128
     p = _params(batch=B, num_q_heads=Hq, num_kv_heads=Hkv, head_dim=d, lengths=FAKE, capacity=cap,
                 max_seq_len=cap)
     n = L.kvq_decode_workspace_size(ctypes.byref(p))
@@ -168,11 +173,30 @@ def test_matrix_core_plan_by_workspace(L, B):
         items = 4 * S + B if flat else S
         assert n == 256 * 1024 + _ru(items * Hq * 2 * 4) + _ru(items * Hq * d * 4)
     else:
-        assert info.split_plan == kvq.SPLITS_SCHEDULE
+        in_kernel = 512 // Hkv < B <= 512 and B * Hkv <= (8 if cap >= 2048 else 4) * 512
+        assert info.split_plan == (kvq.SPLITS_IN_KERNEL if in_kernel else kvq.SPLITS_SCHEDULE)
         items = B + (512 + Hkv - 1) // Hkv + 1
-        sched = _ru((4 + 8 * items + 2 * B) * 4)
+        sched = 0 if in_kernel else _ru((4 + 8 * items + 2 * B) * 4)
         assert n == 256 * 1024 + sched + _ru(items * Hq * 2 * 4) + _ru(items * Hq * d * 4)
-    assert (B in (512, 65)) == (flat and B > 64)
+    assert ((B, cap) in ((512, 512), (65, 512))) == (flat and B > 64)
+
+
+def test_schedule_launch_switch():
+    """KVQ_SCHEDULE_LAUNCH=1 (read once per process) keeps the schedule launch
+    where the decode kernel would derive the schedule itself."""
+    code = ("import importlib, sys; sys.path.insert(0, '.'); "
+            "kvq = importlib.import_module('cuda-operators_amd.kvq'); "
+            "p = kvq.DecodeParams(batch=300, num_q_heads=8, num_kv_heads=2, head_dim=128, capacity=8192, "
+            "max_seq_len=8192, lengths=4096, q=4096, k_cache=4096, v_cache=4096, k_scale=4096, v_scale=4096, "
+            "out=4096, num_splits=0); print(kvq.decode_plan(p).split_plan)")
+    got = {}
+    for flag in ("0", "1"):
+        env = dict(os.environ, KVQ_SCHEDULE_LAUNCH=flag)
+        r = subprocess.run([sys.executable, "-c", code], cwd=REPO, env=env, capture_output=True, text=True,
+                           timeout=120)
+        assert r.returncode == 0, r.stderr
+        got[flag] = int(r.stdout.strip().splitlines()[-1])
+    assert got == {"0": kvq.SPLITS_IN_KERNEL, "1": kvq.SPLITS_SCHEDULE}
 
 
 def test_append_and_quantize_reject_before_hip(L):
@@ -399,6 +423,8 @@ def test_decode_plan_kernels(L):
     i = plan(1, 32, 8, 128, 131072)                                              # cfg3
     assert (i.kernel, i.split_plan, i.splits) == (kvq.KERNEL_DECODE_MFMA, kvq.SPLITS_STATIC, 32)
     i = plan(256, 64, 8, 128, 4096, lengths=A)                                   # cfg4
+    assert (i.kernel, i.heads_per_group, i.split_plan) == (kvq.KERNEL_DECODE_MFMA, 8, kvq.SPLITS_IN_KERNEL)
+    i = plan(513, 64, 8, 128, 4096, lengths=A)
     assert (i.kernel, i.heads_per_group, i.split_plan) == (kvq.KERNEL_DECODE_MFMA, 8, kvq.SPLITS_SCHEDULE)
     assert plan(1, 8, 8, 64, 1024).splits == 1                                   # cfg0
     assert plan(1, 8, 8, 96, 1024).kernel == kvq.KERNEL_DECODE_GENERIC

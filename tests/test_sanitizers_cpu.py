@@ -4,7 +4,7 @@
   with both sanitizers into tests/sanitize/kvq_host_check, which sweeps the
   public C ABI with device-pointer stand-ins and never launches a kernel; it
   runs once per planner switch (KVQ_FORCE_KERNEL, KVQ_FLAT_PLAN,
-  KVQ_DEBUG_SYNC).
+  KVQ_SCHEDULE_LAUNCH, KVQ_DEBUG_SYNC).
 - The CPU oracle and every planted-mistake variant are built with both
   sanitizers (oracle/Makefile `sanitize`) and tests/test_oracle.py runs against
   them in a child Python with the gcc ASan runtime preloaded.
@@ -30,7 +30,7 @@ REPORTS = ("ERROR: AddressSanitizer", "ERROR: LeakSanitizer", "runtime error:", 
 
 def _san_env(**extra):
     env = dict(os.environ)
-    for k in ("KVQ_FORCE_KERNEL", "KVQ_FLAT_PLAN", "KVQ_DEBUG_SYNC", "LD_PRELOAD"):
+    for k in ("KVQ_FORCE_KERNEL", "KVQ_FLAT_PLAN", "KVQ_SCHEDULE_LAUNCH", "KVQ_DEBUG_SYNC", "LD_PRELOAD"):
         env.pop(k, None)
     env["ASAN_OPTIONS"] = "halt_on_error=1:detect_leaks=1"
     env["UBSAN_OPTIONS"] = "halt_on_error=1:print_stacktrace=1"
@@ -58,7 +58,7 @@ def host_check():
 
 
 @pytest.mark.parametrize("switch", [{}, {"KVQ_FORCE_KERNEL": "valu"}, {"KVQ_FORCE_KERNEL": "generic"},
-                                    {"KVQ_FLAT_PLAN": "0"}, {"KVQ_DEBUG_SYNC": "1"}],
+                                    {"KVQ_FLAT_PLAN": "0"}, {"KVQ_SCHEDULE_LAUNCH": "1"}, {"KVQ_DEBUG_SYNC": "1"}],
                          ids=lambda s: ",".join(f"{k}={v}" for k, v in s.items()) or "default")
 def test_host_planner_and_validation_clean(host_check, switch):
     r = subprocess.run([host_check], env=_san_env(**switch), capture_output=True, text=True, timeout=300)
