@@ -96,12 +96,14 @@ def test_opcheck_decode(o):
                           test_utils=("test_schema", "test_faketensor"))
 
 
-@pytest.mark.parametrize("G,B", [(1, 4), (1, 80), (8, 4), (8, 80)])
+@pytest.mark.parametrize("G,B", [(1, 4), (1, 80), (8, 4), (8, 80), (8, 300), (8, 600)])
 def test_decode_graph_capture_replays(o, G, B):
     """One ragged decode step captured once and replayed three times; q
     changes eagerly between replays.  4 sequences: one launch that plans its
-    splits itself; 80 sequences: the split-schedule launch, then decode (FMA
-    kernel for G = 1, matrix-core kernel for G = 8)."""
+    splits itself; 80: the split-schedule launch, then the FMA decode (G = 1),
+    or the flattened tile plan (matrix-core kernel, G = 8); 300: the
+    matrix-core kernel derives the split schedule itself (one launch); 600:
+    the schedule launch, then the matrix-core decode."""
     rng = np.random.default_rng(6 + G + B)
     Hkv, cap, d = 2, 1024, 128
     lengths = rng.integers(1, cap + 1, B).astype(np.int32)
@@ -118,6 +120,10 @@ def test_decode_graph_capture_replays(o, G, B):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         out = torch.ops.kvq.decode(*args())
+    info = kvq.decode_plan(kvq.decode_params(g[0], g[1], g[2], g[3], g[4], out, lengths=g[5], max_seq_len=cap))
+    want = {(1, 4): kvq.SPLITS_IN_KERNEL, (1, 80): kvq.SPLITS_SCHEDULE, (8, 4): kvq.SPLITS_IN_KERNEL,
+            (8, 80): kvq.SPLITS_TILES, (8, 300): kvq.SPLITS_IN_KERNEL, (8, 600): kvq.SPLITS_SCHEDULE}
+    assert info.split_plan == want[(G, B)]
     for rep in range(3):
         g[0].copy_(up(rng.standard_normal(p["q"].shape).astype(np.float32)))
         torch.cuda.synchronize()
