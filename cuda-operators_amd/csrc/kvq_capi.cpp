@@ -274,7 +274,8 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
                 static_cast<long>(B) * U <=
                     static_cast<long>(max_len >= kvq::kLptLongTokens ? kvq::kLptMaxRounds : kvq::kLptMaxRounds / 2) *
                         p.sched_target &&
-                (gran & (gran - 1)) == 0 && p.sched_target < (1 << 23) && max_len <= (1 << 30) && lpt_enabled();
+                (gran & (gran - 1)) == 0 && (p.sched_target & (p.sched_target - 1)) == 0 && max_len <= (1 << 30) &&
+                lpt_enabled();
         const size_t recs = static_cast<size_t>(p.sched_items) * Hq;
         p.counter_bytes = kCounterBytes;
         p.sched_bytes =
@@ -333,6 +334,7 @@ void bind_workspace(DecodeArgs& a, const DecodePlan& p, void* ws) {
     a.counters = p.counters ? reinterpret_cast<int*>(base) : nullptr;
     a.sched = p.scheduled && !p.lpt ? reinterpret_cast<const int*>(base + p.counter_bytes) : nullptr;
     a.lpt_target = p.lpt ? p.sched_target : 0;
+    a.lpt_target_log2 = p.lpt ? __builtin_ctz(static_cast<unsigned>(p.sched_target)) : 0;
     a.sched_items = p.sched_items;
     a.fit_items = p.fit ? p.sched_items : 0;
     a.flat = p.flat ? 1 : 0;

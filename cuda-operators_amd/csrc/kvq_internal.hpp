@@ -57,7 +57,8 @@ struct DecodeArgs {
     int chunk;               // tokens per split (static splits)
     int nsg;                 // head groups per kv head (G / heads per workgroup)
     int lpt_target;          // > 0: the matrix-core kernel derives the split schedule itself (locate_lpt)
-                             // for this many workgroups per round (the schedule kernel's target)
+                             // for this many workgroups per round (the schedule kernel's target) ...
+    int lpt_target_log2;     // ... a power of two, 2^lpt_target_log2
     float scale_log2;        // softmax_scale * log2(e)
 };
 

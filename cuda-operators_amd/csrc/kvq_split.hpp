@@ -159,7 +159,9 @@ struct LptScratch {
     int len[kLptMaxSeqs];
     int rec[kLptMaxSeqs];  // first record of each sequence (when some sequence splits)
     int hist[kSizeClasses];
-    int red[5][kLptWaves];  // per wave: length sum (low 20 bits, the rest), max; splits, whole chunks
+    unsigned long long total;  // length sum, counted by one atomic per wave
+    int longest;               // longest length, likewise
+    int red[2][kLptWaves];     // per wave: splits, whole chunks
 };
 
 // Lowest set lane of a wave mask, 0 for an empty mask (index clamp).
@@ -202,6 +204,10 @@ __device__ inline bool locate_lpt(const DecodeArgs& a, SplitWork& w, LptScratch&
         for (int i = 0; i < kSizeClasses * kLptGroups / kLptThreads; i++) bits[t + i * kLptThreads] = 0ull;
         if (t < kSizeClasses) s.hist[t] = 0;
     };
+    if (t == 0) {
+        s.total = 0ull;
+        s.longest = 0;
+    }
     auto add_class = [&](int b, int c) {
         atomicAdd(&s.hist[c], 1);
         atomicOr(&s.bits[c][b / kWave], 1ull << (b % kWave));
@@ -231,26 +237,18 @@ __device__ inline bool locate_lpt(const DecodeArgs& a, SplitWork& w, LptScratch&
     const int hi = wave_inclusive_scan(static_cast<int>(sum >> 20));
     const int wm = wave_inclusive_max_nonneg(mx);
     if (lane == kWave - 1) {
-        s.red[0][wave] = lo;
-        s.red[1][wave] = hi;
-        s.red[2][wave] = wm;
+        atomicAdd(&s.total, (static_cast<unsigned long long>(static_cast<unsigned>(hi)) << 20) + static_cast<unsigned>(lo));
+        atomicMax(&s.longest, wm);
     }
     __syncthreads();
-    long long total = 0;
-    int longest = 0;
-#pragma unroll
-    for (int v = 0; v < kLptWaves; v++) {
-        total += (static_cast<long long>(s.red[1][v]) << 20) + s.red[0][v];
-        longest = max(longest, s.red[2][v]);
-    }
+    const long long total = static_cast<long long>(s.total);
+    const int longest = s.longest;
     // chunk = min(cmax, max(gran, round_up(ceil(total * U / target), gran)))
-    // without 64-bit divides (gran is a power of two): below target * cmax
-    // the numerator is under 2^53 and the target under 2^23, so the double
-    // quotient is never rounded across an integer.
+    // without divides: gran and the target are powers of two.
     const long long num = total * U;
     int chunk = cmax;
-    if (num < static_cast<long long>(a.lpt_target) * cmax) {
-        const int want = static_cast<int>(ceil(static_cast<double>(num) / static_cast<double>(a.lpt_target)));
+    if (num < (static_cast<long long>(cmax) << a.lpt_target_log2)) {
+        const int want = static_cast<int>((num + (1ll << a.lpt_target_log2) - 1) >> a.lpt_target_log2);
         chunk = min(cmax, max(gran, static_cast<int>((static_cast<unsigned>(want) + gm) & ~gm)));
     }
 
@@ -286,16 +284,16 @@ __device__ inline bool locate_lpt(const DecodeArgs& a, SplitWork& w, LptScratch&
         const int in = wave_inclusive_scan(nt);
         const int inf = wave_inclusive_scan(ft);
         if (lane == kWave - 1) {
-            s.red[3][wave] = in;
-            s.red[4][wave] = inf;
+            s.red[0][wave] = in;
+            s.red[1][wave] = inf;
         }
         __syncthreads();
         int r = in - nt, f = inf - ft, whole = 0;
 #pragma unroll
         for (int v = 0; v < kLptWaves; v++) {
-            r += v < wave ? s.red[3][v] : 0;
-            f += v < wave ? s.red[4][v] : 0;
-            whole += s.red[4][v];
+            r += v < wave ? s.red[0][v] : 0;
+            f += v < wave ? s.red[1][v] : 0;
+            whole += s.red[1][v];
         }
         if (item >= whole + B) return false;
 #pragma unroll
