@@ -241,19 +241,25 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     int base = t0 + __builtin_amdgcn_readfirstlane(wave) * Geo::WSTEP;  // wave-uniform
     // In a paged cache (power-of-two pages here) the next tile's block-table
     // entry is fetched one tile ahead and only turned into a row when that tile
-    // loads, so the scalar load's latency stays off the load path.  The index is
-    // clamped to this sequence's last token: the table is never read past the
-    // sequence's own entries.
+    // loads, so the load's latency stays off the load path.  It is a vector
+    // load: vector loads complete in order, so the wait for it leaves the
+    // tile loads issued after it in flight (a scalar load shares its counter
+    // with LDS traffic and comes back out of order).  The index is clamped to
+    // this sequence's last token: the table is never read past the sequence's
+    // own entries.
+    const buf_rsrc tabr =
+        make_rsrc(PAGED ? a.pages.table + static_cast<size_t>(b) * a.pages.max_pages : nullptr,
+                  PAGED ? static_cast<unsigned>(a.pages.max_pages) * 4u : 0u);
     auto page_entry = [&](int t) -> int {
         if constexpr (PAGED)
-            return a.pages.table[static_cast<size_t>(b) * a.pages.max_pages + (min(t, tend - 1) >> a.pages.shift)];
+            return __builtin_amdgcn_raw_buffer_load_b32(tabr, (min(t, tend - 1) >> a.pages.shift) * 4, 0, 0);
         else return 0;
     };
     int pg_next = page_entry(base);
     auto next_row = [&](int nb) -> size_t {  // row of the tile at nb - BSTEP; prefetch nb's entry
         const int tb = nb - Geo::BSTEP;
         if constexpr (PAGED) {
-            const int page = min(max(pg_next, 0), a.pages.num_pages - 1);
+            const int page = min(max(__builtin_amdgcn_readfirstlane(pg_next), 0), a.pages.num_pages - 1);
             pg_next = page_entry(nb);
             return (static_cast<size_t>(page) * a.Hkv + kvh) * a.pages.size + (tb & (a.pages.size - 1));
         } else {

@@ -896,6 +896,17 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             lvsr = make_rsrc(a.vs + row0, cap * 4u);
         }
     };
+    // Paged: the page id of the cursor's next tile in the same sequence is
+    // fetched with each tile's loads (a vector load issued before them, so
+    // waiting for it leaves them in flight) and used when that tile loads; a
+    // move to another sequence looks its first page up at once.  Page sizes
+    // are powers of two here; indices past a row are clamped into it.
+    int pf_b = -1, pf_base = 0, pf_page = 0;
+    auto table_load = [&](int b, int base) {
+        const buf_rsrc tabr = make_rsrc(a.pages.table + static_cast<size_t>(b) * a.pages.max_pages,
+                                        static_cast<unsigned>(a.pages.max_pages) * 4u);
+        return __builtin_amdgcn_raw_buffer_load_b32(tabr, min(base >> a.pages.shift, a.pages.max_pages - 1) * 4, 0, 0);
+    };
     auto load_tile = [&](Tile& Tt, int b, int base, bool none) {
         buf_rsrc kr, vr, ksr, vsr;
         int ko, so;
@@ -903,7 +914,13 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             kr = vr = ksr = vsr = make_rsrc(a.k, 0u);
             ko = so = 0;
         } else if constexpr (PAGED) {
-            const size_t rp = cache_row(a.pages, a.Hkv, a.cap, b, kvh, base);
+            int id = pf_page;
+            if (b != pf_b || base != pf_base) id = table_load(b, base);
+            const int page = min(max(__builtin_amdgcn_readfirstlane(id), 0), a.pages.num_pages - 1);
+            pf_b = b;
+            pf_base = base + kMTile;
+            pf_page = table_load(b, pf_base);
+            const size_t rp = (static_cast<size_t>(page) * a.Hkv + kvh) * a.pages.size + (base & (a.pages.size - 1));
             const unsigned rem = static_cast<unsigned>(a.pages.size - (base & (a.pages.size - 1)));
             kr = make_rsrc(a.k + rp * D, rem * D);
             vr = make_rsrc(a.v + rp * D, rem * D);
