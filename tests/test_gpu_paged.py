@@ -217,3 +217,34 @@ def test_paged_uniform_length(o, G, page):
     torch.cuda.synchronize()
     ref = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], max_seq_len=L, k_new=kn, v_new=vn)[0]
     assert np.array_equal(_bits(down(out)), _bits(ref))
+
+
+@pytest.mark.parametrize("page", [32, 128])
+def test_paged_in_kernel_schedule_bitwise(o, page):
+    """A ragged batch past one round of items (B = 100, 8 work units per
+    sequence): the matrix-core kernel derives the split schedule itself and
+    fetches each tile's block-table entry one tile ahead; with fused append,
+    identical bits to the contiguous layout (same plan), and the oracle."""
+    rng = np.random.default_rng(900 + page)
+    B, Hkv, G, cap, d = 100, 8, 4, 1024, 64
+    lengths = rng.integers(0, cap + 1, B).astype(np.int32)
+    lengths[:3] = [cap, 0, 1]
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, dist="student_t", lengths=lengths)
+    kn = rng.standard_normal((B, Hkv, d)).astype(np.float32)
+    vn = rng.standard_normal((B, Hkv, d)).astype(np.float32)
+    kp, vp, ksp, vsp, table = to_pages(rng, p["k"], p["v"], p["ks"], p["vs"], lengths, page)
+    got, gkp, gvp, gksp, gvsp, dec = paged_decode(p["q"], kp, vp, ksp, vsp, table, lengths, k_new=kn, v_new=vn,
+                                                  max_seq_len=cap)
+    ref, rk, rv, rks, rvs = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths, k_new=kn,
+                                        v_new=vn)
+    assert np.array_equal(_bits(got), _bits(ref))
+    k2, v2, ks2, vs2 = from_pages(gkp, gvp, gksp, gvsp, table, lengths, p["k"].shape)
+    for x, y in ((k2, rk), (v2, rv)):
+        for b in range(B):
+            assert np.array_equal(x[b, :, : lengths[b]], y[b, :, : lengths[b]])
+    for x, y in ((ks2, rks), (vs2, rvs)):
+        for b in range(B):
+            assert np.array_equal(_bits(x[b, :, : lengths[b]]), _bits(y[b, :, : lengths[b]]))
+    o.append(kn, vn, p["k"], p["v"], p["ks"], p["vs"], positions=lengths - 1)
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert_close(got, want, what=f"paged in-kernel schedule page={page}")
