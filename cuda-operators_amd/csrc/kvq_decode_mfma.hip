@@ -1222,6 +1222,14 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
                 set_load_seq(lb);
             }
             load_tile(Tn, lb, (t + 1 - lE) * kMTile, !more);
+            if constexpr (PAGED) {
+                // Tile t + 2 starts the next sequence: its first page instead.
+                if (more && t + 2 < te && t + 2 == lE + ln) {
+                    pf_b = seq_of(t + 2);
+                    pf_base = 0;
+                    pf_page = table_load(pf_b, 0);
+                }
+            }
             if (switched) load_q(lb);
             if (app && more && t + 1 == lE + ln - 1) load_new(lb);
             int8_t* vt = s_v[wv][it & 1];
