@@ -11,16 +11,24 @@ Timing protocol:
   * inputs resident in HBM; the caches rotate over R replicas with
     R * KV_bytes >= 512 MiB (R >= 3) so steps read HBM, not the 256 MB
     Infinity Cache; a cache-warm single-replica figure is reported separately;
-  * W untimed warm-up steps, then more untimed steps until --settle-ms of
-    wall time has passed (sustained load first, so clocks and power state
-    are at steady state), then exactly K steps between two HIP events on the
-    launch stream, synchronised on both sides -> ms_per_step, value;
+  * every configuration is set up first; then W untimed warm-up steps and
+    untimed steps of each configuration until --settle-ms of wall time
+    (sustained load first, so clocks and power state are at steady state);
+  * --rounds rounds: round r visits the configurations in an order rotated by
+    r, and times each for exactly its step count (K for the headline) between
+    two HIP events on the launch stream, synchronised on both sides, after
+    --round-settle-ms of its own untimed steps.  The median round gives
+    ms_per_step and value; "rounds" lists every round with min and max;
   * every step is exactly one launch of the decode kernel, so the timed
     region / K is that kernel's average duration -> roofline.achieved; a
-    second pass brackets every launch with its own events (reported as
+    further pass brackets every launch with its own events (reported as
     kernel_us_isolated: launches spaced by the event records);
   * cpu_baseline: the CPU oracle (same fp32 math as the reference's
-    cpu_reference, OpenMP over heads) on the host copy of the same step.
+    cpu_reference, OpenMP over heads) on the host copy of the same step;
+    the checked step is also compared with the float64 oracle ("vs_f64":
+    the GPU's error and the fp32 oracle's own, against the same yardstick);
+  * verify_line() re-derives value, GB/s, fractions and the round summaries
+    from the line's own fields before it is printed.
 
 Besides the headline (cfg1), the same protocol runs every configuration of
 BASELINE.json (cfg0..cfg4, --configs) and reports each under "configs": us per
@@ -76,6 +84,10 @@ def parse():
                     help="configurations to time besides the headline, comma-separated ('none': headline only)")
     ap.add_argument("--config-steps", type=int, default=200,
                     help="timed steps per extra configuration (at least --steps)")
+    ap.add_argument("--rounds", type=int, default=3,
+                    help="timed rounds per configuration, in rotated order (the median round is reported)")
+    ap.add_argument("--round-settle-ms", type=float, default=20.0,
+                    help="untimed steps of a configuration right before each of its timed rounds")
     ap.add_argument("--config-cpu-budget", type=float, default=3.0,
                     help="max seconds for each extra configuration's CPU baseline")
     ap.add_argument("--calib", action="store_true",
@@ -121,6 +133,7 @@ def cpu_baseline(prob, budget_s, min_runs=5):
         return o.decode_f32(q, k, v, ks, vs, lengths=lengths)
 
     ref = step()  # warm-up; also the checked step's expected output
+    ref64 = o.decode_f64(q, k, v, ks, vs, lengths=lengths)  # the same step in double precision
     times, t_start = [], time.perf_counter()
     while len(times) < min_runs or (time.perf_counter() - t_start < 2.0 and len(times) < 50):
         t0 = time.perf_counter()
@@ -139,7 +152,7 @@ def cpu_baseline(prob, budget_s, min_runs=5):
                    f"{prob.B}x{prob.Hq} query heads), median of {len(times)} runs: {t * 1e6:.0f} us/step"),
     }
     base.update(host_info())
-    return base, ref
+    return base, ref, ref64
 
 
 def check_step(got, ref):
@@ -153,6 +166,20 @@ def check_step(got, ref):
     return {"max_abs_err": float(err.max()) if finite else None,
             "max_tol_frac": float((err / (1e-4 + 1e-3 * np.abs(r))).max()) if finite else None,
             "within_tolerance": finite and bool(np.all(err <= 1e-4 + 1e-3 * np.abs(r)))}
+
+
+def f64_errors(got, ref32, ref64):
+    """Both the GPU's and the fp32 oracle's distance from the float64 oracle
+    on the same step (as the reference's scan harness judges every
+    implementation against an FP64 oracle, benchmarks/selective_scan/bench.cpp:85-99):
+    which of the two carries the error the fp32 comparison reports."""
+    import numpy as np
+    r = np.asarray(ref64, np.float64)
+    g = np.abs(np.asarray(got, np.float64) - r)
+    c = np.abs(np.asarray(ref32, np.float64) - r)
+    scale = 1e-4 + 1e-3 * np.abs(r)
+    return {"gpu_max_abs": float(g.max()), "oracle_f32_max_abs": float(c.max()),
+            "gpu_max_tol_frac": float((g / scale).max()), "oracle_f32_max_tol_frac": float((c / scale).max())}
 
 
 def _sha256_files(paths):
@@ -261,98 +288,179 @@ def kernel_name(kvq, dec):
     return name + (f", {info.splits} splits" if info.splits > 1 else ", unsplit")
 
 
-def time_config(args, torch, kvq, synth, name, steps, settle_ms, page_size=0):
-    """Build config `name` (seeded, on the GPU), then W warm-up steps, settle,
-    K timed steps over rotated replicas, a per-launch pass and a cache-warm
-    pass.  Returns (result dict, the Problem, replica 0's output)."""
-    stream = torch.cuda.current_stream()
-    base = synth.make(name, seed=args.seed, device="cuda")
-    kv_bytes = base.kv_bytes()
-    alloc_bytes = base.B * base.Hkv * base.cap * (2 * base.d + 8)
-    R = args.replicas or max(3, math.ceil(512 * 2**20 / alloc_bytes))
-    reps = [base]
-    for _ in range(R - 1):
-        c = synth.Problem(base.name, base.B, base.Hq, base.Hkv, base.d, base.cap, base.lengths_host,
-                          base.q.clone(), base.k.clone(), base.v.clone(), base.ks.clone(), base.vs.clone(),
-                          base.lengths, base.k_new, base.v_new)
-        reps.append(c)
-    outs = [torch.empty_like(base.q) for _ in reps]
-    if page_size > 0:
-        decs = [paged_decoder(kvq, p, o, page_size, args.splits, args.seed + i, args.page_order)
-                for i, (p, o) in enumerate(zip(reps, outs))]
-    else:
-        decs = [kvq.Decoder(p.q, p.k, p.v, p.ks, p.vs, o, lengths=p.lengths,
-                            max_seq_len=(0 if p.uniform else p.max_len) or p.cap,
-                            num_splits=args.splits, k_new=p.k_new, v_new=p.v_new)
-                for p, o in zip(reps, outs)]
-    torch.cuda.synchronize()
+class ConfigRun:
+    """One configuration set up for timing: the seeded problem on the GPU,
+    R cache replicas (R * KV bytes >= 512 MiB, R >= 3) so steps read HBM
+    rather than the 256 MB Infinity Cache, one output per replica and one
+    prepared launch per replica."""
 
-    # Launches go to the current stream by its raw handle: one foreign call
-    # per step, so host work between launches stays small (heavier per-launch
-    # host work measurably slowed the running kernels on MI355X).
-    sh = stream.cuda_stream
-    t_warm = time.perf_counter()
-    for i in range(args.warmup):
-        decs[i % R](sh)
-    torch.cuda.synchronize()
-    settle = 0
-    while (time.perf_counter() - t_warm) * 1e3 < settle_ms:
-        for _ in range(50):
-            decs[(args.warmup + settle) % R](sh)
-            settle += 1
+    def __init__(self, args, torch, kvq, synth, name, steps, page_size=0):
+        self.torch, self.name, self.steps = torch, name, steps
+        base = synth.make(name, seed=args.seed, device="cuda")
+        self.base = base
+        self.kv_bytes = base.kv_bytes()
+        alloc_bytes = base.B * base.Hkv * base.cap * (2 * base.d + 8)
+        R = args.replicas or max(3, math.ceil(512 * 2**20 / alloc_bytes))
+        reps = [base]
+        for _ in range(R - 1):
+            reps.append(synth.Problem(base.name, base.B, base.Hq, base.Hkv, base.d, base.cap, base.lengths_host,
+                                      base.q.clone(), base.k.clone(), base.v.clone(), base.ks.clone(),
+                                      base.vs.clone(), base.lengths, base.k_new, base.v_new))
+        self.R = R
+        self.outs = [torch.empty_like(base.q) for _ in reps]
+        if page_size > 0:
+            self.decs = [paged_decoder(kvq, p, o, page_size, args.splits, args.seed + i, args.page_order)
+                         for i, (p, o) in enumerate(zip(reps, self.outs))]
+        else:
+            self.decs = [kvq.Decoder(p.q, p.k, p.v, p.ks, p.vs, o, lengths=p.lengths,
+                                     max_seq_len=(0 if p.uniform else p.max_len) or p.cap,
+                                     num_splits=args.splits, k_new=p.k_new, v_new=p.v_new)
+                         for p, o in zip(reps, self.outs)]
+        self.kernel = kernel_name(kvq, self.decs[0])
+        self.splits = self.decs[0].params.num_splits or "auto"
+        self.workload = (f"{name}: B{base.B} Hq{base.Hq} Hkv{base.Hkv} d{base.d} "
+                         f"L{'U' if not base.uniform else ''}{base.max_len}"
+                         f"{' +append' if base.k_new is not None else ''}")
+        self.settle_steps = 0
+        self.rounds_ms = []
+        self.i = 0
         torch.cuda.synchronize()
 
-    # Pass 1: K steps between two events on the launch stream (the timed region).
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for i in range(steps):
-        decs[i % R](sh)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms_per_step = e0.elapsed_time(e1) / steps
+    def launch(self, n, sh):
+        # Launches go to the stream by its raw handle: one foreign call per
+        # step, so host work between launches stays small (heavier per-launch
+        # host work measurably slowed the running kernels on MI355X).
+        for _ in range(n):
+            self.decs[self.i % self.R](sh)
+            self.i += 1
 
-    # Pass 2: every launch between its own events (kernel duration).
-    n2 = min(steps, 100)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n2)]
-    for i, (a, b) in enumerate(ev):
-        a.record(stream)
-        decs[i % R](sh)
-        b.record(stream)
-    torch.cuda.synchronize()
-    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    def settle(self, sh, ms):
+        """Untimed steps until `ms` of wall time has passed (sustained load)."""
+        t0 = time.perf_counter()
+        while (time.perf_counter() - t0) * 1e3 < ms:
+            self.launch(50, sh)
+            self.settle_steps += 50
+            self.torch.cuda.synchronize()
 
-    # Pass 3: cache-warm (single replica, no rotation), labelled separately.
-    w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for _ in range(5):
-        decs[0](sh)
-    w0.record(stream)
-    for _ in range(n2):
-        decs[0](sh)
-    w1.record(stream)
-    torch.cuda.synchronize()
-    warm_ms = w0.elapsed_time(w1) / n2
+    def timed(self, stream):
+        """Exactly `steps` steps between two events on the launch stream,
+        synchronised on both sides; ms per step."""
+        torch = self.torch
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        self.launch(self.steps, stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / self.steps
+        self.rounds_ms.append(ms)
+        return ms
 
-    gbps = kv_bytes / (ms_per_step * 1e-3) / 1e9
-    res = {
-        "workload": f"{name}: B{base.B} Hq{base.Hq} Hkv{base.Hkv} d{base.d} "
-                    f"L{'U' if not base.uniform else ''}{base.max_len}"
-                    f"{' +append' if base.k_new is not None else ''}",
-        "kernel": kernel_name(kvq, decs[0]),
-        "us_per_step": round(ms_per_step * 1e3, 3),
-        "GB/s": round(gbps, 2),
-        "frac": round(gbps / HBM_PEAK_GBPS, 4),
-        "kv_bytes_per_step": kv_bytes,
-        "steps": steps,
-        "settle_steps": settle,
-        "replicas": R,
-        "kernel_us_isolated": round(kern_ms * 1e3, 3),
-        "cache_warm_us_per_step": round(warm_ms * 1e3, 3),
-        "splits": decs[0].params.num_splits or "auto",
-    }
-    out0 = outs[0]
-    del decs, reps
-    return res, base, out0
+    def extras(self, stream):
+        """Per-launch events (kernel duration) and a cache-warm pass over a
+        single replica (labelled separately)."""
+        torch = self.torch
+        sh = stream.cuda_stream
+        n2 = min(self.steps, 100)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n2)]
+        for i, (a, b) in enumerate(ev):
+            a.record(stream)
+            self.decs[i % self.R](sh)
+            b.record(stream)
+        torch.cuda.synchronize()
+        kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+        w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(5):
+            self.decs[0](sh)
+        w0.record(stream)
+        for _ in range(n2):
+            self.decs[0](sh)
+        w1.record(stream)
+        torch.cuda.synchronize()
+        return kern_ms, w0.elapsed_time(w1) / n2
+
+    def result(self, stream):
+        """The configuration's line entry: the median round is the figure,
+        min and max show the spread."""
+        kern_ms, warm_ms = self.extras(stream)
+        ms = statistics.median(self.rounds_ms)
+        gbps = self.kv_bytes / (ms * 1e-3) / 1e9
+        return {
+            "workload": self.workload,
+            "kernel": self.kernel,
+            "us_per_step": round(ms * 1e3, 3),
+            "GB/s": round(gbps, 2),
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "kv_bytes_per_step": self.kv_bytes,
+            "steps": self.steps,
+            "rounds": {"n": len(self.rounds_ms),
+                       "us_per_step": [round(x * 1e3, 3) for x in self.rounds_ms],
+                       "median": round(ms * 1e3, 3),
+                       "min": round(min(self.rounds_ms) * 1e3, 3),
+                       "max": round(max(self.rounds_ms) * 1e3, 3)},
+            "settle_steps": self.settle_steps,
+            "replicas": self.R,
+            "kernel_us_isolated": round(kern_ms * 1e3, 3),
+            "cache_warm_us_per_step": round(warm_ms * 1e3, 3),
+            "splits": self.splits,
+        }
+
+    def release(self):
+        out0 = self.outs[0]
+        base = self.base
+        self.decs = self.outs = self.base = None
+        return base, out0
+
+
+def rotated(names, r):
+    """Round r runs the configurations starting at the r-th, so no
+    configuration always follows the same one (as the reference's harness
+    shuffles its order per round, benchmarks/selective_scan/run.py:166-194)."""
+    k = r % len(names)
+    return names[k:] + names[:k]
+
+
+def verify_line(line):
+    """Problems with a bench line, re-derived from its own fields (as the
+    reference's verify_results.py:21-72 recomputes its summaries from the raw
+    rows): empty when the line is consistent."""
+    bad = []
+
+    def near(a, b, rel=2e-3, what=""):
+        if a is None or b is None or abs(a - b) > rel * max(abs(a), abs(b), 1e-12):
+            bad.append(f"{what}: {a} vs {b}")
+
+    kvb = line["config"]["kv_bytes_per_step"]
+    near(line["value"], kvb / (line["ms_per_step"] * 1e-3) / 1e9, what="value = KV bytes / ms_per_step")
+    near(line["us_per_step"], line["ms_per_step"] * 1e3, what="us_per_step")
+    near(line["pct_hbm_peak"], 100.0 * line["value"] / HBM_PEAK_GBPS, what="pct_hbm_peak")
+    rf = line["roofline"]
+    near(rf["frac"], rf["achieved"] / rf["peak"], what="roofline.frac")
+    near(rf["achieved"], line["value"], what="roofline.achieved")
+    near(rf["peak"], HBM_PEAK_GBPS, what="roofline.peak")
+    if rf["bytes_per_launch"] != kvb:
+        bad.append("roofline.bytes_per_launch != config.kv_bytes_per_step")
+    rounds = line.get("rounds")
+    if rounds:
+        us = rounds["us_per_step"]
+        if len(us) != rounds["n"]:
+            bad.append("rounds: n != len(us_per_step)")
+        near(rounds["median"], statistics.median(us), what="rounds.median")
+        near(rounds["min"], min(us), what="rounds.min")
+        near(rounds["max"], max(us), what="rounds.max")
+        near(line["us_per_step"], rounds["median"], what="us_per_step = median round")
+    for name, c in (line.get("configs") or {}).items():
+        near(c["GB/s"], c["kv_bytes_per_step"] / (c["us_per_step"] * 1e-6) / 1e9, what=f"{name} GB/s")
+        near(c["frac"], c["GB/s"] / HBM_PEAK_GBPS, rel=5e-3, what=f"{name} frac")
+        r = c.get("rounds")
+        if r:
+            near(c["us_per_step"], statistics.median(r["us_per_step"]), what=f"{name} median round")
+            if not r["min"] <= c["us_per_step"] <= r["max"]:
+                bad.append(f"{name}: median outside [min, max]")
+        if "within_tolerance" in c and c["max_tol_frac"] is not None:
+            if c["within_tolerance"] != (c["max_tol_frac"] <= 1.0):
+                bad.append(f"{name}: within_tolerance disagrees with max_tol_frac")
+    return bad
 
 
 def main():
@@ -370,17 +478,48 @@ def main():
     kvq.lib()  # fail loudly if the HIP library is missing
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
 
-    head, base, out0 = time_config(args, torch, kvq, synth, args.config, args.steps, args.settle_ms,
-                                   args.page_size)
+    # Every configuration is set up first (seeded problems and replicas, about
+    # 10 GB in all), then timed in rounds: round r runs them in rotated order,
+    # each after a short settle on its own steps, each for exactly its step
+    # count.  The headline's figure is its median round.
+    wanted = [] if args.configs.strip() in ("", "none") else [c.strip() for c in args.configs.split(",")]
+    head_key = "__head__"
+    runs = {head_key: ConfigRun(args, torch, kvq, synth, args.config, args.steps, args.page_size)}
+    for name in wanted:
+        if name == args.config and args.page_size == 0:
+            continue  # the headline is this configuration
+        runs[name] = ConfigRun(args, torch, kvq, synth, name, max(args.steps, args.config_steps))
+    # Sustained load first (clocks and power at steady state): W warm-up steps
+    # of the headline, then --settle-ms of wall time across the configurations.
+    runs[head_key].launch(args.warmup, sh)
+    torch.cuda.synchronize()
+    for key, r in runs.items():
+        r.settle(sh, args.settle_ms if key == head_key else min(args.settle_ms, 100.0))
+    order = list(runs)
+    for rnd in range(args.rounds):
+        for key in rotated(order, rnd):
+            runs[key].settle(sh, args.round_settle_ms)
+            runs[key].timed(stream)
+    results = {key: r.result(stream) for key, r in runs.items()}
+
+    head = results[head_key]
     kv_bytes = head["kv_bytes_per_step"]
     ms_per_step = head["us_per_step"] * 1e-3
-    head_check = None
-    head_cpu = None
-    if not args.no_cpu:
-        head_cpu, ref = cpu_baseline(base, args.cpu_budget)
-        head_check = check_step(out0.cpu().numpy(), ref)
-    del base, out0
+    checks = {}
+    cpus = {}
+    for key, r in runs.items():
+        base, out0 = r.release()
+        if not args.no_cpu:
+            budget = args.cpu_budget if key == head_key else args.config_cpu_budget
+            cpus[key], ref, ref64 = cpu_baseline(base, budget, min_runs=5 if key == head_key else 3)
+            got = out0.cpu().numpy()
+            checks[key] = check_step(got, ref)
+            checks[key]["vs_f64"] = f64_errors(got, ref, ref64)
+        del base, out0
+    runs.clear()
     torch.cuda.empty_cache()
 
     if args.calib:
@@ -433,6 +572,7 @@ def main():
                        else "contiguous"),
             "parallelism": "single GPU",
         },
+        "rounds": head["rounds"],
         "roofline": {
             "bound": "hbm",
             "kernel": head["kernel"],
@@ -449,34 +589,29 @@ def main():
                        "GB/s": round(kv_bytes / (head["cache_warm_us_per_step"] * 1e-6) / 1e9, 2),
                        "note": "single replica, Infinity-Cache resident; not the headline"},
     }
-    if head_cpu is not None:
-        line["cpu_baseline"] = head_cpu
-        line["parity"] = head_check
+    if head_key in cpus:
+        line["cpu_baseline"] = cpus[head_key]
+        line["parity"] = checks[head_key]
 
-    # Every other configuration under the same protocol.
-    wanted = [] if args.configs.strip() in ("", "none") else [c.strip() for c in args.configs.split(",")]
     configs = {}
     for name in wanted:
-        if name == args.config and args.page_size == 0:
-            res = {k: head[k] for k in ("workload", "kernel", "us_per_step", "GB/s", "frac", "kv_bytes_per_step",
-                                        "steps", "replicas", "kernel_us_isolated", "cache_warm_us_per_step")}
-            if head_cpu is not None:
-                res["cpu_baseline"] = head_cpu
-                res.update(head_check)
-        else:
-            res, base, out0 = time_config(args, torch, kvq, synth, name, max(args.steps, args.config_steps),
-                                          min(args.settle_ms, 200.0))
-            if not args.no_cpu:
-                res["cpu_baseline"], ref = cpu_baseline(base, args.config_cpu_budget, min_runs=3)
-                res.update(check_step(out0.cpu().numpy(), ref))
-            del base, out0
-            torch.cuda.empty_cache()
+        key = head_key if (name == args.config and args.page_size == 0) else name
+        res = dict(results[key])
+        res.pop("settle_steps", None)
+        res.pop("splits", None) if key == head_key else None
+        if key in cpus:
+            res["cpu_baseline"] = cpus[key]
+            res.update(checks[key])
         tr = traffic_all.get(name)
         res["traffic"] = tr.get("hbm_bytes_per_launch") if tr else None
         configs[name] = res
     if configs:
         line["configs"] = configs
     line["provenance"] = provenance(torch, kvq)
+    problems = verify_line(line)
+    if problems:  # a line that contradicts itself is a bench bug: say so, keep the line
+        line["verify"] = problems
+        print("bench.py: inconsistent line: " + "; ".join(problems), file=sys.stderr)
     print(json.dumps(line), flush=True)
 
 

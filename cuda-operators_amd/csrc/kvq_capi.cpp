@@ -144,15 +144,52 @@ int forced_kernel() {
     return k;
 }
 
-// Every launching entry point returns through here.
+// The library's code objects are built for gfx950 only.  Checked once per
+// device before its first launch, as the reference warns once about an
+// untuned architecture (kv_cache/KV_int8_split_optimized.cu:57-65); here
+// another architecture cannot run the kernels at all, so the call fails with
+// hipErrorInvalidDevice after one stderr line.
+std::mutex g_arch_mutex;
+signed char g_arch_state[64];  // 0 unknown, 1 gfx950, -1 other
+
+hipError_t arch_check() {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_arch_mutex);
+    if (g_arch_state[dev] == 0) {
+        hipDeviceProp_t prop;
+        err = hipGetDeviceProperties(&prop, dev);
+        if (err != hipSuccess) return err;
+        const bool ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
+                        (prop.gcnArchName[6] == '\0' || prop.gcnArchName[6] == ':');
+        g_arch_state[dev] = ok ? 1 : -1;
+        if (!ok)
+            fprintf(stderr, "[kvq] device %d is %s; libkvq is built for gfx950 (MI355X) only\n", dev,
+                    prop.gcnArchName);
+    }
+    return g_arch_state[dev] > 0 ? hipSuccess : hipErrorInvalidDevice;
+}
+
+// Every launching entry point returns through here: the device check, the
+// launches, then (KVQ_DEBUG_SYNC) the stream's completion status.
+hipError_t finish_call(hipError_t err, hipStream_t stream);
+template <class Launch>
+hipError_t checked_call(hipStream_t stream, Launch&& launch) {
+    const hipError_t err = arch_check();
+    if (err != hipSuccess) return err;
+    return finish_call(launch(), stream);
+}
+
 hipError_t finish_call(hipError_t err, hipStream_t stream) {
     if (err != hipSuccess || !debug_sync()) return err;
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     err = hipStreamIsCapturing(stream, &st);
     if (err != hipSuccess || st != hipStreamCaptureStatusNone) return err;
-    err = hipStreamSynchronize(stream);
-    if (err != hipSuccess) return err;
-    return hipGetLastError();
+    // The launchers already returned their launch status; the caller's own
+    // pending error (hipGetLastError) is left for the caller.
+    return hipStreamSynchronize(stream);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -219,11 +256,14 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
     //   full-length sequences (B300 L 1-40: 26 / 34 us; B1000 L 0-256: 122 /
     //   125 us).
     // Record ids run to waves + B per query head.
+    // The kernel counts the virtual stream (every tile at full length plus
+    // kFlatSwitchTiles per sequence) in 32-bit integers.
     const long flat_tiles = static_cast<long>(B) * ((static_cast<long>(max_len) + kvq::kMfmaTile - 1) / kvq::kMfmaTile);
     const bool flat_shape = B <= kvq::kFitMaxSeqs || flat_tiles <= 16L * kvq::kMfmaWaves * fit_items;
+    const bool flat_counts = flat_tiles + static_cast<long>(kvq::kFlatSwitchTiles) * B <= INT_MAX;
     if (ragged && requested == 0 && fused && p.kernel == kvq::Kernel::Mfma && fit_items >= 1 &&
-        B <= kvq::kFlatMaxSeqs && 4 * B >= fit_items && flat_shape && static_cast<long>(B) * U <= kMaxCounters &&
-        max_len <= (1 << 30) && flat_enabled()) {
+        B <= kvq::kFlatMaxSeqs && 4 * B >= fit_items && flat_shape && flat_counts &&
+        static_cast<long>(B) * U <= kMaxCounters && max_len <= KVQ_MAX_SEQ_LEN && flat_enabled()) {
         p.fit = true;
         p.flat = true;
         p.counters = true;
@@ -238,7 +278,7 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
         return p;
     }
     if (ragged && requested == 0 && fused && fit_kernel && units <= kMaxCounters && B <= kvq::kFitMaxSeqs &&
-        B <= fit_items && max_len <= (1 << 30)) {
+        B <= fit_items && max_len <= KVQ_MAX_SEQ_LEN) {
         // Small ragged batch: every workgroup plans the batch itself from the
         // lengths (one round of at most fit_items items per work unit; no
         // schedule launch).
@@ -274,7 +314,7 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
                 static_cast<long>(B) * U <=
                     static_cast<long>(max_len >= kvq::kLptLongTokens ? kvq::kLptMaxRounds : kvq::kLptMaxRounds / 2) *
                         p.sched_target &&
-                (gran & (gran - 1)) == 0 && (p.sched_target & (p.sched_target - 1)) == 0 && max_len <= (1 << 30) &&
+                (gran & (gran - 1)) == 0 && (p.sched_target & (p.sched_target - 1)) == 0 && max_len <= KVQ_MAX_SEQ_LEN &&
                 lpt_enabled();
         const size_t recs = static_cast<size_t>(p.sched_items) * Hq;
         p.counter_bytes = kCounterBytes;
@@ -344,7 +384,9 @@ void bind_workspace(DecodeArgs& a, const DecodePlan& p, void* ws) {
     a.part_acc = p.acc_bytes ? reinterpret_cast<float*>(base + ml + p.ml_bytes) : nullptr;
 }
 
-bool shape_ok(int H, int N, int d) { return H > 0 && N > 0 && d > 0 && d <= KVQ_MAX_HEAD_DIM; }
+bool shape_ok(int H, int N, int d) {
+    return H > 0 && N > 0 && N <= KVQ_MAX_SEQ_LEN && d > 0 && d <= KVQ_MAX_HEAD_DIM;
+}
 
 // Reference-ABI problem ([H,N,d], one query per head) as a batched problem.
 DecodeArgs reference_args(const float* Q, const int8_t* K, const int8_t* V, const float* ks,
@@ -399,7 +441,7 @@ hipError_t reference_launch(const float* Q, const int8_t* K, const int8_t* V, co
     a.chunk = p.chunk;
     a.nsg = p.nsg;
     bind_workspace(a, p, S);
-    return finish_call(kvq::launch_decode(a, p, stream), stream);
+    return checked_call(stream, [&] { return kvq::launch_decode(a, p, stream); });
 }
 
 // Library-owned, per-device split workspace for the legacy `solve` ABI.  Grown
@@ -465,6 +507,7 @@ bool decode_params_ok(const kvq_decode_params* p) {
     if (p->max_seq_len < 0 || p->num_splits < 0) return false;
     if (!p->lengths && p->max_seq_len == 0) return false;
     if (p->max_seq_len > p->capacity) return false;
+    if ((p->max_seq_len > 0 ? p->max_seq_len : p->capacity) > KVQ_MAX_SEQ_LEN) return false;
     if (!p->q || !p->k_cache || !p->v_cache || !p->k_scale || !p->v_scale || !p->out) return false;
     if ((p->k_new == nullptr) != (p->v_new == nullptr)) return false;
     const long long units = static_cast<long long>(p->batch) * p->num_q_heads;
@@ -563,6 +606,7 @@ bool paged_params_ok(const kvq_paged_decode_params* p) {
     const long long cap = static_cast<long long>(p->max_pages_per_seq) * p->page_size;
     if (cap > INT_MAX || p->max_seq_len < 0 || p->max_seq_len > cap || p->num_splits < 0) return false;
     if (!p->lengths && p->max_seq_len == 0) return false;
+    if ((p->max_seq_len > 0 ? p->max_seq_len : cap) > KVQ_MAX_SEQ_LEN) return false;
     if (!p->block_table || !p->q || !p->k_pages || !p->v_pages || !p->k_scale_pages || !p->v_scale_pages ||
         !p->out)
         return false;
@@ -792,8 +836,9 @@ void solve(const float* Q, const int8_t* K_int8, const int8_t* V_int8, const flo
         return;
     }
     if (!shape_ok(num_heads, seq_len, head_dim) || static_cast<long long>(num_heads) * seq_len > INT_MAX) {
-        fprintf(stderr, "[kvq] solve: invalid shape: num_heads=%d, seq_len=%d, head_dim=%d (head_dim <= %d)\n",
-                num_heads, seq_len, head_dim, KVQ_MAX_HEAD_DIM);
+        fprintf(stderr,
+                "[kvq] solve: invalid shape: num_heads=%d, seq_len=%d, head_dim=%d (head_dim <= %d, seq_len <= %d)\n",
+                num_heads, seq_len, head_dim, KVQ_MAX_HEAD_DIM, KVQ_MAX_SEQ_LEN);
         return;
     }
     DecodeArgs a = reference_args(Q, K_int8, V_int8, k_scale, v_scale, output, num_heads, seq_len, head_dim);
@@ -802,10 +847,12 @@ void solve(const float* Q, const int8_t* K_int8, const int8_t* V_int8, const flo
     a.splits = p.splits;
     a.chunk = p.chunk;
     a.nsg = p.nsg;
-    const hipError_t err = finish_call(with_solve_workspace(plan_bytes(p), [&](void* ws) {
-        bind_workspace(a, p, ws);
-        return kvq::launch_decode(a, p, nullptr);
-    }), nullptr);
+    const hipError_t err = checked_call(nullptr, [&] {
+        return with_solve_workspace(plan_bytes(p), [&](void* ws) {
+            bind_workspace(a, p, ws);
+            return kvq::launch_decode(a, p, nullptr);
+        });
+    });
     if (err != hipSuccess) fprintf(stderr, "[kvq] solve: HIP error: %s (%s)\n", hipGetErrorName(err), hipGetErrorString(err));
 }
 
@@ -829,7 +876,7 @@ size_t kvq_decode_workspace_size(const kvq_decode_params* p) {
 hipError_t kvq_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (workspace_bytes == 0) return hipSuccess;
     if (!workspace) return hipErrorInvalidValue;
-    return finish_call(kvq::launch_fill_zero(workspace, workspace_bytes, stream), stream);
+    return checked_call(stream, [&] { return kvq::launch_fill_zero(workspace, workspace_bytes, stream); });
 }
 
 hipError_t kvq_decode_launch(const kvq_decode_params* p, void* workspace, size_t workspace_bytes,
@@ -838,7 +885,7 @@ hipError_t kvq_decode_launch(const kvq_decode_params* p, void* workspace, size_t
     const DecodePlan plan = decode_plan(p);
     const size_t need = plan_bytes(plan);
     if (need > 0 && (!workspace || workspace_bytes < need)) return hipErrorInvalidValue;
-    return finish_call(decode_run(p, plan, workspace, stream), stream);
+    return checked_call(stream, [&] { return decode_run(p, plan, workspace, stream); });
 }
 
 hipError_t kvq_decode_launch_noalloc(const kvq_decode_params* p, hipStream_t stream) {
@@ -846,12 +893,14 @@ hipError_t kvq_decode_launch_noalloc(const kvq_decode_params* p, hipStream_t str
     const DecodePlan plan = decode_plan(p);
     const size_t need = plan_bytes(plan);
     if (need > KVQ_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;  // beyond the fixed scratch array
-    void* ws = nullptr;
-    if (need > 0) {
-        const hipError_t err = noalloc_scratch(stream, &ws);
-        if (err != hipSuccess) return err;
-    }
-    return finish_call(decode_run(p, plan, ws, stream), stream);
+    return checked_call(stream, [&] {
+        void* ws = nullptr;
+        if (need > 0) {
+            const hipError_t err = noalloc_scratch(stream, &ws);
+            if (err != hipSuccess) return err;
+        }
+        return decode_run(p, plan, ws, stream);
+    });
 }
 
 hipError_t kvq_append_launch(const kvq_append_params* p, hipStream_t stream) {
@@ -859,11 +908,11 @@ hipError_t kvq_append_launch(const kvq_append_params* p, hipStream_t stream) {
         p->capacity <= 0 || !p->k_new || !p->v_new || !p->k_cache || !p->v_cache || !p->k_scale || !p->v_scale)
         return hipErrorInvalidValue;
     if (static_cast<long long>(p->batch) * p->num_kv_heads > INT_MAX) return hipErrorInvalidValue;
-    return finish_call(kvq::launch_append(p->k_new, p->v_new, p->k_cache, p->v_cache, p->k_scale, p->v_scale,
-                                          p->positions, p->uniform_position, false, p->batch, p->num_kv_heads,
-                                          p->capacity, p->capacity, p->head_dim,
-                                          kvq::PageMap{nullptr, 0, 0, 0, -1}, stream),
-                       stream);
+    return checked_call(stream, [&] {
+        return kvq::launch_append(p->k_new, p->v_new, p->k_cache, p->v_cache, p->k_scale, p->v_scale, p->positions,
+                                  p->uniform_position, false, p->batch, p->num_kv_heads, p->capacity, p->capacity,
+                                  p->head_dim, kvq::PageMap{nullptr, 0, 0, 0, -1}, stream);
+    });
 }
 
 hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, int8_t* q, float* scale,
@@ -887,9 +936,9 @@ hipError_t kvq_quantize_rows_launch(const float* x, int64_t rows, int head_dim, 
         a.nseq = 1;
         a.pages = kvq::PageMap{nullptr, 0, 0, 0, -1};
         a.max_groups = prefill_max_groups();
-        return finish_call(kvq::launch_prefill(a, head_dim, false, true, stream), stream);
+        return checked_call(stream, [&] { return kvq::launch_prefill(a, head_dim, false, true, stream); });
     }
-    return finish_call(kvq::launch_quantize_rows(x, rows, head_dim, q, scale, stream), stream);
+    return checked_call(stream, [&] { return kvq::launch_quantize_rows(x, rows, head_dim, q, scale, stream); });
 }
 
 size_t kvq_paged_decode_workspace_size(const kvq_paged_decode_params* p) {
@@ -928,7 +977,7 @@ hipError_t kvq_paged_decode_launch(const kvq_paged_decode_params* p, void* works
     const float scale = p->softmax_scale > 0.0f ? p->softmax_scale : 1.0f / sqrtf(static_cast<float>(p->head_dim));
     a.scale_log2 = scale * kLog2e;
     bind_workspace(a, plan, workspace);
-    return finish_call(kvq::launch_decode(a, plan, stream), stream);
+    return checked_call(stream, [&] { return kvq::launch_decode(a, plan, stream); });
 }
 
 hipError_t kvq_paged_append_launch(const kvq_paged_append_params* p, hipStream_t stream) {
@@ -940,12 +989,12 @@ hipError_t kvq_paged_append_launch(const kvq_paged_append_params* p, hipStream_t
     if (cap > INT_MAX || static_cast<long long>(p->batch) * p->num_kv_heads > INT_MAX ||
         static_cast<long long>(p->batch) * p->max_pages_per_seq > INT_MAX)
         return hipErrorInvalidValue;
-    return finish_call(
-        kvq::launch_append(p->k_new, p->v_new, p->k_pages, p->v_pages, p->k_scale_pages, p->v_scale_pages,
-                           p->positions, p->uniform_position, false, p->batch, p->num_kv_heads,
-                           static_cast<int>(cap), static_cast<int>(cap), p->head_dim,
-                           page_map(p->block_table, p->page_size, p->max_pages_per_seq, p->num_pages), stream),
-        stream);
+    return checked_call(stream, [&] {
+        return kvq::launch_append(p->k_new, p->v_new, p->k_pages, p->v_pages, p->k_scale_pages, p->v_scale_pages,
+                                  p->positions, p->uniform_position, false, p->batch, p->num_kv_heads,
+                                  static_cast<int>(cap), static_cast<int>(cap), p->head_dim,
+                                  page_map(p->block_table, p->page_size, p->max_pages_per_seq, p->num_pages), stream);
+    });
 }
 
 hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t stream) {
@@ -992,16 +1041,19 @@ hipError_t kvq_prefill_quantize_launch(const kvq_prefill_params* p, hipStream_t 
                              static_cast<long long>(p->batch) * p->max_pages_per_seq * 4 < (1LL << 31));
     const bool vec_ok = tables_fit && aligned16(p->k_new) && aligned16(p->v_new) &&
                         ((reinterpret_cast<uintptr_t>(p->k_cache) | reinterpret_cast<uintptr_t>(p->v_cache)) & 7u) == 0;
-    return finish_call(kvq::launch_prefill(a, p->head_dim, p->dtype == KVQ_DTYPE_BF16, vec_ok, stream), stream);
+    return checked_call(stream,
+                        [&] { return kvq::launch_prefill(a, p->head_dim, p->dtype == KVQ_DTYPE_BF16, vec_ok, stream); });
 }
 
 hipError_t attention_online_launch(const float* Q, const float* K, const float* V, float* output, int M, int N,
                                    int d, hipStream_t stream) {
     if (!attention_args_ok(M, N, d, Q, K, V, output)) return hipErrorInvalidValue;
     const AttnPlan p = attention_plan(M, N, d, attention_aligned(Q, K, V, output), 0);
-    return finish_call(with_attention_workspace(p.bytes(), stream, [&](void* ws) {
-        return attention_run(M, N, d, Q, K, V, output, 1.0f / sqrtf(static_cast<float>(d)), p, ws, stream);
-    }), stream);
+    return checked_call(stream, [&] {
+        return with_attention_workspace(p.bytes(), stream, [&](void* ws) {
+            return attention_run(M, N, d, Q, K, V, output, 1.0f / sqrtf(static_cast<float>(d)), p, ws, stream);
+        });
+    });
 }
 
 size_t kvq_attention_workspace_size(const kvq_attention_params* p) {
@@ -1018,8 +1070,9 @@ hipError_t kvq_attention_launch(const kvq_attention_params* p, void* workspace, 
     if (plan.bytes() > 0 && (!workspace || workspace_bytes < plan.bytes() || !aligned16(workspace)))
         return hipErrorInvalidValue;
     const float scale = p->softmax_scale != 0.0f ? p->softmax_scale : 1.0f / sqrtf(static_cast<float>(p->d));
-    return finish_call(attention_run(p->M, p->N, p->d, p->q, p->k, p->v, p->out, scale, plan, workspace, stream),
-                       stream);
+    return checked_call(stream, [&] {
+        return attention_run(p->M, p->N, p->d, p->q, p->k, p->v, p->out, scale, plan, workspace, stream);
+    });
 }
 
 const char* kvq_version(void) { return "kvq 0.2.0 gfx950"; }
@@ -1036,6 +1089,12 @@ hipError_t kvq_reference_plan(const float* Q, const int8_t* K_int8, const int8_t
 hipError_t kvq_decode_plan(const kvq_decode_params* p, kvq_plan_info* info) {
     if (!info || !decode_params_ok(p)) return hipErrorInvalidValue;
     *info = decode_info(decode_plan(p));
+    return hipSuccess;
+}
+
+hipError_t kvq_paged_decode_plan(const kvq_paged_decode_params* p, kvq_plan_info* info) {
+    if (!info || !paged_params_ok(p)) return hipErrorInvalidValue;
+    *info = decode_info(paged_plan(p));
     return hipSuccess;
 }
 

@@ -787,7 +787,13 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     const int tb = real_of(flat_start(fs, gw));
     const int te = real_of(flat_start(fs, gw + 1));
     if (big) win_load(tb < T ? find_seq(tb) : 0);
-    auto seq_of = [&](int t) {  // the sequence holding tile t < T; moves the window when t is past it
+    // The sequence holding tile t < T; moves the window when t is past it.
+    // With kFlatSwitchTiles >= 1 the planner's bound (at most 16 tiles per
+    // wave at full length beyond 64 sequences) keeps every range below
+    // 16 * (1 + kFlatSwitchTiles) virtual tiles, fewer than 64 sequences
+    // need, so the move is a safeguard that no planned launch takes.
+    static_assert(kFlatSwitchTiles >= 1, "switch tiles bound the sequences one wave range spans");
+    auto seq_of = [&](int t) {
         if (big && t >= wend) win_load(find_seq(t));
         return wb0 + static_cast<int>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < wcount && e_l <= t))) -
                1;
@@ -1224,8 +1230,10 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
             load_tile(Tn, lb, (t + 1 - lE) * kMTile, !more);
             if constexpr (PAGED) {
                 // Tile t + 2 starts the next sequence: its first page instead.
+                // Looked up without moving the window, which must keep the
+                // compute cursor's sequence for its length below.
                 if (more && t + 2 < te && t + 2 == lE + ln) {
-                    pf_b = seq_of(t + 2);
+                    pf_b = (big && t + 2 >= wend) ? find_seq(t + 2) : seq_of(t + 2);
                     pf_base = 0;
                     pf_page = table_load(pf_b, 0);
                 }

@@ -26,6 +26,7 @@ ATTN_LIB_PATH = os.path.join(HERE, "libkvq_attention.so")
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
 MAX_HEAD_DIM = 4096
+MAX_SEQ_LEN = 1 << 30  # KVQ_MAX_SEQ_LEN
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -118,7 +119,7 @@ EXPORTS = ("solve", "kv_int8_split_launch", "kv_int8_simple_launch", "kvq_decode
            "kvq_paged_decode_workspace_size", "kvq_paged_decode_launch", "kvq_paged_append_launch",
            "kvq_prefill_quantize_launch", "attention_online_launch", "kvq_attention_workspace_size",
            "kvq_attention_launch", "kvq_version", "kvq_reference_plan", "kvq_decode_plan", "kvq_attention_plan",
-           "kvq_diagnostics", "kvq_decode_launch_noalloc")
+           "kvq_diagnostics", "kvq_decode_launch_noalloc", "kvq_paged_decode_plan")
 
 
 class KvqError(RuntimeError):
@@ -173,6 +174,8 @@ def lib() -> ctypes.CDLL:
         L.kvq_reference_plan.restype = _int
         L.kvq_decode_plan.argtypes = [ctypes.POINTER(DecodeParams), ctypes.POINTER(PlanInfo)]
         L.kvq_decode_plan.restype = _int
+        L.kvq_paged_decode_plan.argtypes = [ctypes.POINTER(PagedDecodeParams), ctypes.POINTER(PlanInfo)]
+        L.kvq_paged_decode_plan.restype = _int
         L.kvq_attention_plan.argtypes = [ctypes.POINTER(AttentionParams), ctypes.POINTER(PlanInfo)]
         L.kvq_attention_plan.restype = _int
         L.kvq_diagnostics.restype = _int
@@ -516,6 +519,13 @@ def decode_plan(p: DecodeParams) -> PlanInfo:
     return info
 
 
+def paged_decode_plan(p: PagedDecodeParams) -> PlanInfo:
+    """Plan of kvq_paged_decode_launch for p (host-only)."""
+    info = PlanInfo()
+    _check("kvq_paged_decode_plan", lib().kvq_paged_decode_plan(ctypes.byref(p), ctypes.byref(info)))
+    return info
+
+
 def attention_plan(p: AttentionParams) -> PlanInfo:
     """Plan of kvq_attention_launch for p (host-only)."""
     info = PlanInfo()
@@ -545,5 +555,5 @@ __all__ = ["lib", "version", "solve", "kv_int8_split_launch", "DecodeParams", "A
            "append", "quantize_rows", "kv_bytes", "KvqError", "EXPORTS", "PagedDecodeParams",
            "PagedAppendParams", "PagedDecoder", "paged_append", "PrefillParams", "prefill", "DTYPE_F32",
            "DTYPE_BF16", "AttentionParams", "attention_online", "attention_params", "attention_workspace_size",
-           "attention", "PlanInfo", "reference_plan", "decode_plan", "attention_plan", "diagnostics",
+           "attention", "PlanInfo", "reference_plan", "decode_plan", "paged_decode_plan", "attention_plan", "diagnostics",
            "attention_lib", "attention_solve", "decode_launch_noalloc", "NOALLOC_SCRATCH_BYTES"]

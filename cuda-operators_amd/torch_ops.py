@@ -25,10 +25,14 @@ allocates nothing once its workspace exists.
 Workspaces are cached per (operator, device, stream) and grown on demand:
 launches on one stream are ordered, so they may share one; launches on
 different streams get different ones.  A workspace is zero-filled by a kernel
-(never a memset) when it is allocated, also inside a graph capture, where the
-fill becomes part of the graph.  A workspace that a later, larger call
+(never a memset) when it is allocated.  A workspace that a later, larger call
 supersedes is kept alive (never freed), because graphs captured before still
-write to it on every replay.
+write to it on every replay.  A graph capture uses the stream's cached
+workspace when it is large enough; otherwise the capture allocates one of its
+own, whose zero-fill is recorded in the graph and runs only when the graph is
+replayed, so that workspace belongs to that graph alone: it is never cached
+for eager calls (which could run before the first replay) nor for other
+captures.
 """
 from __future__ import annotations
 
@@ -53,18 +57,21 @@ _retired: list = []
 def _workspace(key, nbytes: int, device) -> Tensor:
     with _ws_lock:
         ws = _workspaces.get(key)
-        if ws is None or ws.numel() < nbytes:
-            # During a capture torch allocates from the graph's private pool
-            # and the zero-fill kernel is captured too (replays re-zero the
-            # counters, which every completed launch leaves at zero anyway).
-            size = max(nbytes, 2 * ws.numel() if ws is not None else 0, 1)
-            new = torch.empty(size, dtype=torch.uint8, device=device)
-            kvq.workspace_init(new, size)
-            if ws is not None:
-                _retired.append(ws)
-            ws = new
-            _workspaces[key] = ws
-        return ws
+        if ws is not None and ws.numel() >= nbytes:
+            return ws
+        size = max(nbytes, 2 * ws.numel() if ws is not None else 0, 1)
+        new = torch.empty(size, dtype=torch.uint8, device=device)
+        kvq.workspace_init(new, size)
+        if torch.cuda.is_current_stream_capturing():
+            # Allocated from the graph's private pool; the zero-fill kernel is
+            # part of the graph and has not run yet.  Only this graph may use
+            # it (kept alive for its replays).
+            _retired.append(new)
+            return new
+        if ws is not None:
+            _retired.append(ws)
+        _workspaces[key] = new
+        return new
 
 
 def _opt(t: Optional[Tensor]):

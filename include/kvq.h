@@ -40,6 +40,14 @@ extern "C" {
  * the tuned kernels; any other value up to this bound runs a generic kernel). */
 #define KVQ_MAX_HEAD_DIM 4096
 
+/* Longest sequence any decode entry point attends to, in tokens: seq_len of
+ * the reference entry points, and the effective max_seq_len of the extension
+ * (max_seq_len, or the capacity when it is 0).  The kernels count tokens and
+ * tiles in 32-bit integers; beyond this bound the call is rejected with
+ * hipErrorInvalidValue (solve: one stderr line).  Capacities and page tables
+ * may be larger. */
+#define KVQ_MAX_SEQ_LEN (1 << 30)
+
 /* ===================== Part 1: reference entry points ===================== */
 
 /* Replaces `solve`, kv_cache/KV_int8.cu:306-316 (also KV_int8_single_buffer.cu:260-270,
@@ -59,8 +67,8 @@ void solve(const float* Q, const int8_t* K_int8, const int8_t* V_int8,
  * per-split partial (max, sum, acc[d]) records, so at most seq_len/(head_dim+2)
  * splits per head are used (1 split needs no scratch at all).
  * Returns hipErrorInvalidValue, before any HIP call, for a null pointer,
- * num_heads/seq_len/head_dim <= 0 or head_dim > KVQ_MAX_HEAD_DIM; otherwise the
- * launch status.  Asynchronous on `stream`; the caller checks completion. */
+ * num_heads/seq_len/head_dim <= 0, head_dim > KVQ_MAX_HEAD_DIM or
+ * seq_len > KVQ_MAX_SEQ_LEN; otherwise the launch status.  Asynchronous on `stream`; the caller checks completion. */
 hipError_t kv_int8_split_launch(const float* Q, const int8_t* K_int8, const int8_t* V_int8,
                                 const float* k_scale, const float* v_scale, float* output,
                                 int num_heads, int seq_len, int head_dim, float* S,
@@ -343,6 +351,8 @@ hipError_t kvq_reference_plan(const float* Q, const int8_t* K_int8, const int8_t
                               int seq_len, int head_dim, kvq_plan_info* info);
 /* The plan of kvq_decode_launch for p. */
 hipError_t kvq_decode_plan(const kvq_decode_params* p, kvq_plan_info* info);
+/* The plan of kvq_paged_decode_launch for p. */
+hipError_t kvq_paged_decode_plan(const kvq_paged_decode_params* p, kvq_plan_info* info);
 /* The plan of kvq_attention_launch for p (attention_online_launch: p with
  * softmax_scale 0 and num_splits 0). */
 hipError_t kvq_attention_plan(const kvq_attention_params* p, kvq_plan_info* info);

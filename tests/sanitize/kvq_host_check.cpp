@@ -12,14 +12,21 @@
 //     kv_cache/KV_int8_split_optimized.cu:266-267), splits <= N / (d + 2);
 //   * kvq_*_workspace_size equals the plan query's workspace_bytes, and is 0
 //     exactly when the parameters are rejected;
-//   * a workspace one byte short is rejected with hipErrorInvalidValue.
+//   * a workspace one byte short is rejected with hipErrorInvalidValue;
+//   * lengths above KVQ_MAX_SEQ_LEN are rejected, and every accepted plan's
+//     32-bit token and tile counts stay in range (paged_bounds).
 // Exit status 0 and a last line "OK <checks>" when everything holds.
+#include <algorithm>
 #include <climits>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <vector>
 
 #include "kvq.h"
+#include "kvq_device.hpp"    // kWave
+#include "kvq_internal.hpp"  // kMfmaTile, kFlatSwitchTiles: the tile-stream plan's geometry
 
 namespace {
 
@@ -159,6 +166,16 @@ void decode_plans() {
                                 expect(info.kernel >= KVQ_KERNEL_DECODE_GENERIC &&
                                            info.kernel <= KVQ_KERNEL_DECODE_MFMA,
                                        "decode kernel id", B, d, info.kernel);
+                                if (info.split_plan == KVQ_SPLITS_TILES && B > kvq::kWave) {
+                                    // Beyond one wave of sequences no wave range may span 64
+                                    // sequences (each holds kFlatSwitchTiles virtual tiles).
+                                    const long U = static_cast<long>(g[1]) * (g[0] / g[1] / info.heads_per_group);
+                                    const long waves = kvq::kMfmaWaves * (256 / U);
+                                    const long stream = static_cast<long>(B) * ((L + kvq::kMfmaTile - 1) / kvq::kMfmaTile) +
+                                                        static_cast<long>(kvq::kFlatSwitchTiles) * B;
+                                    expect((stream + waves - 1) / waves < static_cast<long>(kvq::kWave) * kvq::kFlatSwitchTiles,
+                                           "tile-stream ranges span fewer than 64 sequences", B, d, L, stream);
+                                }
                                 if (need > 0) {
                                     expect(kvq_decode_launch(&p, fake<void>(), need - 1, nullptr) ==
                                                hipErrorInvalidValue,
@@ -243,6 +260,82 @@ void paged_plans() {
     expect(kvq_paged_decode_workspace_size(nullptr) == 0, "paged workspace null params");
     expect(kvq_paged_decode_launch(nullptr, fake<void>(), 1 << 20, nullptr) == hipErrorInvalidValue,
            "paged launch null params");
+}
+
+// Paged caches may span up to INT_MAX tokens per sequence, but a decode call
+// attends to at most KVQ_MAX_SEQ_LEN.  Every accepted plan must keep the
+// counts its kernel holds in 32-bit integers in range:
+//   * the flattened tile stream (KVQ_SPLITS_TILES): every sequence's tiles at
+//     the longest length plus kFlatSwitchTiles virtual tiles per sequence;
+//   * static splits: the last split's end, splits * chunk;
+//   * every plan: the longest length itself.
+void paged_bounds() {
+    const int batches[] = {1, 2, 16, 33, 63, 64};
+    const int groups[][2] = {{32, 8}, {64, 8}, {8, 2}, {32, 32}};
+    const int pages[] = {32, 128, 4096, 1 << 16, 1 << 20};
+    const long long wants[] = {1 << 20, (1LL << 30) - 32, 1LL << 30, (1LL << 30) + 1, 1LL << 31};
+    kvq_plan_info info;
+    long flat_seen = 0;
+    for (int B : batches) {
+        for (const auto& g : groups) {
+            for (int d : {64, 128}) {
+                for (int ps : pages) {
+                    for (long long want : wants) {
+                        // Table row long enough for `want` tokens, capped at INT_MAX tokens.
+                        const long long mpp_ll = std::min<long long>((want + ps - 1) / ps, INT_MAX / ps);
+                        const int mpp = static_cast<int>(mpp_ll);
+                        const long long cap = static_cast<long long>(mpp) * ps;
+                        for (int msl_kind = 0; msl_kind < 2; msl_kind++) {
+                            for (int s : {0, 2, 7}) {
+                                kvq_paged_decode_params p{};
+                                p.batch = B;
+                                p.num_q_heads = g[0];
+                                p.num_kv_heads = g[1];
+                                p.head_dim = d;
+                                p.page_size = ps;
+                                p.num_pages = 1 << 16;
+                                p.max_pages_per_seq = mpp;
+                                p.max_seq_len = msl_kind == 0 ? 0 : static_cast<int>(std::min<long long>(want, cap));
+                                p.block_table = fake<int32_t>();
+                                p.lengths = fake<int32_t>();
+                                p.q = fake<float>();
+                                p.k_pages = fake<int8_t>();
+                                p.v_pages = fake<int8_t>();
+                                p.k_scale_pages = fake<float>();
+                                p.v_scale_pages = fake<float>();
+                                p.out = fake<float>();
+                                p.num_splits = s;
+                                const long long eff = p.max_seq_len > 0 ? p.max_seq_len : cap;
+                                const hipError_t e = kvq_paged_decode_plan(&p, &info);
+                                const bool table_ok = static_cast<long long>(B) * mpp <= INT_MAX;
+                                expect((e == hipSuccess) == (eff <= KVQ_MAX_SEQ_LEN && table_ok),
+                                       "paged plan accepted iff length <= KVQ_MAX_SEQ_LEN", B, ps, eff, e);
+                                expect(kvq_paged_decode_workspace_size(&p) == (e == hipSuccess ? info.workspace_bytes : 0),
+                                       "paged workspace == plan", B, ps, eff);
+                                if (e != hipSuccess) continue;
+                                if (info.split_plan == KVQ_SPLITS_TILES) {
+                                    flat_seen++;
+                                    const long long stream =
+                                        B * ((eff + kvq::kMfmaTile - 1) / kvq::kMfmaTile) +
+                                        static_cast<long long>(kvq::kFlatSwitchTiles) * B;
+                                    expect(stream <= INT_MAX, "tile stream fits int32", B, ps, eff, stream >> 20);
+                                }
+                                if (info.split_plan == KVQ_SPLITS_STATIC && info.splits > 1) {
+                                    expect(static_cast<long long>(info.splits) * info.chunk <= INT_MAX,
+                                           "last split end fits int32", B, ps, eff, info.splits);
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    }
+    // Unless a planner switch keeps it off (KVQ_FORCE_KERNEL, KVQ_FLAT_PLAN=0).
+    const char* flat_env = std::getenv("KVQ_FLAT_PLAN");
+    const bool flat_on = (kvq_diagnostics() >> 4) == 0 && !(flat_env && std::strcmp(flat_env, "0") == 0);
+    expect(flat_seen > 0 || !flat_on, "the sweep reaches the tile-stream plan", flat_seen);
+    expect(kvq_paged_decode_plan(nullptr, &info) == hipErrorInvalidValue, "paged plan null params");
 }
 
 void attention_plans() {
@@ -374,6 +467,7 @@ int main() {
     reference_abi();
     decode_plans();
     paged_plans();
+    paged_bounds();
     attention_plans();
     writers();
     if (g_fails) {

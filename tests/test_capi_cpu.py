@@ -94,6 +94,38 @@ def test_reference_launch_rejects_before_hip(L, fn, bad):
     assert getattr(L, fn)(*_ref_args(**bad)) == INVALID
 
 
+@pytest.mark.parametrize("fn", ["kv_int8_split_launch", "kv_int8_simple_launch"])
+def test_reference_launch_sequence_bound(L, fn):
+    """seq_len up to KVQ_MAX_SEQ_LEN = 2^30 plans; one more is rejected (the
+    kernels count tokens in 32-bit integers)."""
+    info = kvq.PlanInfo()
+    assert L.kvq_reference_plan(FAKE, FAKE, FAKE, 1, kvq.MAX_SEQ_LEN, 1, ctypes.byref(info)) == 0
+    assert L.kvq_reference_plan(FAKE, FAKE, FAKE, 1, kvq.MAX_SEQ_LEN + 1, 1, ctypes.byref(info)) == INVALID
+    assert getattr(L, fn)(*_ref_args(H=1, N=kvq.MAX_SEQ_LEN + 1, d=1)) == INVALID
+
+
+def test_decode_sequence_bound(L):
+    """The effective max_seq_len (max_seq_len, or the capacity when it is 0)
+    may not exceed KVQ_MAX_SEQ_LEN; a larger capacity with a bound under it is
+    fine, for contiguous and paged caches."""
+    info = kvq.PlanInfo()
+    big = kvq.MAX_SEQ_LEN + 64
+    for cap, msl, ok in ((big, 0, False), (big, kvq.MAX_SEQ_LEN + 1, False), (big, kvq.MAX_SEQ_LEN, True),
+                         (kvq.MAX_SEQ_LEN, 0, True)):
+        p = _params(batch=1, capacity=cap, max_seq_len=msl, lengths=FAKE)
+        assert (L.kvq_decode_plan(ctypes.byref(p), ctypes.byref(info)) == 0) == ok, (cap, msl)
+        assert (L.kvq_decode_workspace_size(ctypes.byref(p)) > 0) == ok, (cap, msl)
+        if not ok:
+            assert L.kvq_decode_launch(ctypes.byref(p), FAKE, 1 << 30, None) == INVALID
+    for mpp, msl, ok in (((1 << 14) + 1, 0, False), ((1 << 14) + 1, kvq.MAX_SEQ_LEN, True), (1 << 14, 0, True)):
+        pp = kvq.PagedDecodeParams(batch=4, num_q_heads=32, num_kv_heads=8, head_dim=128, page_size=1 << 16,
+                                   num_pages=8, max_pages_per_seq=mpp, max_seq_len=msl, block_table=FAKE, lengths=FAKE, q=FAKE, k_pages=FAKE,
+                                   v_pages=FAKE, k_scale_pages=FAKE, v_scale_pages=FAKE, out=FAKE)
+        assert (L.kvq_paged_decode_plan(ctypes.byref(pp), ctypes.byref(info)) == 0) == ok, (mpp, msl)
+        if not ok:
+            assert L.kvq_paged_decode_launch(ctypes.byref(pp), FAKE, 1 << 30, None) == INVALID
+
+
 def test_solve_invalid_prints_and_returns(L, capfd):
     L.solve(None, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 128, 64)
     L.solve(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0, 128, 64)

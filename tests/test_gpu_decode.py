@@ -36,7 +36,7 @@ def _bits(a):
     return np.ascontiguousarray(a).view(np.uint32)
 
 
-def _check_config(o, name, seed, scale_len=1.0, splits=0):
+def _check_config(o, name, seed, scale_len=1.0, splits=0, f64=False):
     p = synth.make(name, seed=seed, scale_len=scale_len)
     h = _host(p)
     out = torch.full(p.q.shape, float("nan"), device=_gpu.dev())
@@ -53,6 +53,13 @@ def _check_config(o, name, seed, scale_len=1.0, splits=0):
         assert np.array_equal(_bits(down(p.vs)), _bits(h["vs"])), "appended v scale differs"
     want = o.decode_f32(h["q"], h["k"], h["v"], h["ks"], h["vs"], lengths=h["lengths"])
     assert_close(got, want, what=f"{name} seed {seed} splits {splits}")
+    if f64:
+        # The float64 oracle as the yardstick for both: the GPU's error may
+        # not exceed twice the fp32 oracle's own (sequential fp32 sums).
+        w64 = o.decode_f64(h["q"], h["k"], h["v"], h["ks"], h["vs"], lengths=h["lengths"])
+        gpu_err = float(np.abs(got.astype(np.float64) - w64).max())
+        ref_err = float(np.abs(want.astype(np.float64) - w64).max())
+        assert gpu_err <= 2.0 * ref_err, f"{name}: |GPU - f64| {gpu_err:.3e} > 2 x |oracle f32 - f64| {ref_err:.3e}"
     return dec
 
 
@@ -67,6 +74,15 @@ def test_config_small(o, name, seed):
 def test_config_full_size(o, name):
     """Every config at its full BASELINE size (seed 17)."""
     _check_config(o, name, 17)
+
+
+@pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg4"])
+def test_config_full_size_against_f64(o, name):
+    """The grouped-query configs (matrix-core kernel: q as int8 limbs, PV
+    weights as f16 hi/lo pairs) at full size against the float64 oracle: the
+    GPU's largest error is at most twice the fp32 oracle's, so an accuracy
+    loss in the matrix-core path shows up inside the 1e-4 + 1e-3 band."""
+    _check_config(o, name, 17, f64=True)
 
 
 @pytest.mark.parametrize("seed", [29, 101])

@@ -195,10 +195,12 @@ def test_big_batch_plan(o, B, cap):
     _check(o, B, Hkv, G, cap, d, lengths, rng, append=True, dist="student_t", what=f"B={B}")
 
 
-def test_window_moves_along_the_range(o):
-    """1500 sequences of 0-32 tokens with a run of 300 empty ones: the wave
-    whose range crosses the run spans more than 64 sequences, so its window
-    moves on."""
+def test_run_of_empty_sequences(o):
+    """1500 sequences of 0-32 tokens with a run of 300 empty ones.  Each empty
+    sequence still holds its kFlatSwitchTiles virtual tiles, so the run is
+    spread over the waves like any other part of the stream (and no wave's
+    range spans 64 sequences: the planner's bound keeps a range below 48
+    virtual tiles, which the host checker asserts)."""
     rng = np.random.default_rng(2000)
     B, Hkv, G, cap, d = 1500, 8, 4, 32, 64
     lengths = rng.integers(0, cap + 1, B).astype(np.int32)

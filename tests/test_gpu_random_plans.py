@@ -7,7 +7,8 @@ requested splits) with merges of 1 to many splits.
 
 Parity as in test_gpu_decode: out[b, hq] = oracle kvq_ref_decode_f32 over the
 first length[b] tokens of kv head hq / G, 1e-4 abs + 1e-3 rel elementwise;
-appended int8 values and scales bit-exact.
+appended int8 values and scales bit-exact, in the contiguous cache or in the
+page pool (where every other byte must be unchanged).
 """
 import numpy as np
 import pytest
@@ -75,6 +76,7 @@ def test_random_plan(o, case):
                          k_new=gkn, v_new=gvn)()
         torch.cuda.synchronize()
         got = down(out)
+        pool = [down(x) for x in g[1:5]]
     else:
         got, gk, gv, gks, gvs = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths,
                                              max_seq_len=cap, splits=splits, k_new=kn, v_new=vn)
@@ -83,5 +85,21 @@ def test_random_plan(o, case):
         if not paged:
             assert np.array_equal(gk, p["k"]) and np.array_equal(gv, p["v"]), f"{what}: appended int8 differs"
             assert np.array_equal(_bits(gks), _bits(p["ks"])) and np.array_equal(_bits(gvs), _bits(p["vs"])), what
+        else:
+            # The page pool after the step: the original pool with each
+            # sequence's token length-1 replaced by the oracle's appended row,
+            # and no other byte changed.
+            want_pool = [x.copy() for x in (kp, vp, ksp, vsp)]
+            for b in range(B):
+                t = int(L[b]) - 1
+                if t < 0:
+                    continue
+                pg, sl = int(table[b, t // paged]), t % paged
+                for wp, src in zip(want_pool, (p["k"], p["v"], p["ks"], p["vs"])):
+                    wp[pg, :, sl] = src[b, :, t]
+            assert np.array_equal(pool[0], want_pool[0]) and np.array_equal(pool[1], want_pool[1]), \
+                f"{what}: paged appended int8 differs"
+            assert np.array_equal(_bits(pool[2]), _bits(want_pool[2])) and \
+                np.array_equal(_bits(pool[3]), _bits(want_pool[3])), f"{what}: paged appended scales differ"
     want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=L)
     assert_close(got, want, what=what)

@@ -217,3 +217,38 @@ def test_graph_replay_after_workspace_growth(o):
         want = o.decode_f32(down(g[0]), p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
         np.testing.assert_allclose(down(out), want, atol=1e-4, rtol=1e-3, err_msg=f"replay {rep}")
         assert all(bool((t == 7.0).all()) for t in guards), f"replay {rep} wrote into freed memory"
+
+
+def test_capture_time_workspace_stays_with_its_graph(o):
+    """A decode step captured on a fresh stream with no eager call before
+    (its workspace is created inside the capture, zero-filled only when the
+    graph replays), then an eager call on the same stream before the first
+    replay: the eager call must not use the capture's workspace, whose
+    arrival counters were never zeroed.  Both the eager result and every
+    replay equal the oracle."""
+    rng = np.random.default_rng(91)
+    Hkv, G, d, B, cap = 2, 4, 128, 4, 1024
+    lengths = np.array([1024, 517, 33, 800], np.int32)
+    p = make_problem(rng, B, Hkv * G, Hkv, cap, d, o.quantize_rows, lengths=lengths)
+    g = [up(x) for x in (p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths)]
+    args = lambda: (g[0], g[1], g[2], g[3], g[4], g[5], cap, 0.0, 0, None, None)
+    s = torch.cuda.Stream()
+    key = ("decode", 0, s.cuda_stream)
+    assert key not in torch_ops._workspaces
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out = torch.ops.kvq.decode(*args())
+    assert key not in torch_ops._workspaces  # the capture's workspace is the graph's own
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    with torch.cuda.stream(s):
+        eager = torch.ops.kvq.decode(*args())
+    s.synchronize()
+    np.testing.assert_allclose(down(eager), want, atol=1e-4, rtol=1e-3)
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(down(out), want, atol=1e-4, rtol=1e-3, err_msg=f"replay {rep}")
+        with torch.cuda.stream(s):
+            eager = torch.ops.kvq.decode(*args())
+        s.synchronize()
+        assert np.array_equal(_bits(down(out)), _bits(down(eager))), f"replay {rep}"
