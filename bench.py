@@ -426,16 +426,21 @@ def verify_line(line):
     rows): empty when the line is consistent."""
     bad = []
 
-    def near(a, b, rel=2e-3, what=""):
-        if a is None or b is None or abs(a - b) > rel * max(abs(a), abs(b), 1e-12):
+    def near(a, b, rel=2e-3, what="", digits=None):
+        # digits: a is rounded to that many decimals, so half a unit of the
+        # last place is allowed as well.
+        tol = rel * max(abs(a or 0.0), abs(b or 0.0), 1e-12)
+        if digits is not None:
+            tol = max(tol, 0.5 * 10.0 ** -digits + 1e-12)
+        if a is None or b is None or abs(a - b) > tol:
             bad.append(f"{what}: {a} vs {b}")
 
     kvb = line["config"]["kv_bytes_per_step"]
     near(line["value"], kvb / (line["ms_per_step"] * 1e-3) / 1e9, what="value = KV bytes / ms_per_step")
     near(line["us_per_step"], line["ms_per_step"] * 1e3, what="us_per_step")
-    near(line["pct_hbm_peak"], 100.0 * line["value"] / HBM_PEAK_GBPS, what="pct_hbm_peak")
+    near(line["pct_hbm_peak"], 100.0 * line["value"] / HBM_PEAK_GBPS, what="pct_hbm_peak", digits=2)
     rf = line["roofline"]
-    near(rf["frac"], rf["achieved"] / rf["peak"], what="roofline.frac")
+    near(rf["frac"], rf["achieved"] / rf["peak"], what="roofline.frac", digits=4)
     near(rf["achieved"], line["value"], what="roofline.achieved")
     near(rf["peak"], HBM_PEAK_GBPS, what="roofline.peak")
     if rf["bytes_per_launch"] != kvb:
@@ -451,7 +456,7 @@ def verify_line(line):
         near(line["us_per_step"], rounds["median"], what="us_per_step = median round")
     for name, c in (line.get("configs") or {}).items():
         near(c["GB/s"], c["kv_bytes_per_step"] / (c["us_per_step"] * 1e-6) / 1e9, what=f"{name} GB/s")
-        near(c["frac"], c["GB/s"] / HBM_PEAK_GBPS, rel=5e-3, what=f"{name} frac")
+        near(c["frac"], c["GB/s"] / HBM_PEAK_GBPS, what=f"{name} frac", digits=4)
         r = c.get("rounds")
         if r:
             near(c["us_per_step"], statistics.median(r["us_per_step"]), what=f"{name} median round")

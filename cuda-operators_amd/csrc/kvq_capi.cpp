@@ -230,6 +230,7 @@ DecodePlan make_plan(int B, int Hq, int Hkv, int d, int max_len, bool aligned, b
         p.sg = 1;
     }
     p.fast = p.kernel != kvq::Kernel::Generic;
+    p.tile = tile;
     p.nsg = p.fast ? G / p.sg : G;
     const long units = p.fast ? static_cast<long>(B) * Hkv * p.nsg : static_cast<long>(B) * Hq;
     const int gran = p.fast ? tile : 64;
@@ -496,6 +497,7 @@ kvq_plan_info decode_info(const DecodePlan& p) {
     r.chunk = r.split_plan == KVQ_SPLITS_STATIC ? p.chunk : 0;
     r.query_block = 0;
     r.workspace_bytes = plan_bytes(p);
+    r.tile_tokens = p.tile;
     return r;
 }
 

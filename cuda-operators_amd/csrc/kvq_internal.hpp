@@ -119,6 +119,7 @@ struct DecodePlan {
     Kernel kernel;
     bool fast;       // a tuned kernel (Valu or Mfma): 16-byte aligned rows
     int sg;          // query heads per workgroup (tuned kernels)
+    int tile;        // tokens one workgroup iteration covers (tuned kernels; 0: generic)
     int nsg;         // G / sg
     int splits;      // splits per sequence (grid dimension)
     int chunk;       // tokens per split

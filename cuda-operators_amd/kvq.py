@@ -107,6 +107,7 @@ class PlanInfo(ctypes.Structure):
     _fields_ = [
         ("kernel", _int), ("heads_per_group", _int), ("splits", _int), ("chunk", _int),
         ("split_plan", _int), ("query_block", _int), ("workspace_bytes", ctypes.c_size_t),
+        ("tile_tokens", _int),
     ]
 
 

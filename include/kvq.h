@@ -342,6 +342,8 @@ typedef struct kvq_plan_info {
     int split_plan;         /* KVQ_SPLITS_* */
     int query_block;        /* attention: queries per workgroup; decode: 0 */
     size_t workspace_bytes; /* workspace (or scratch S) bytes the launch uses */
+    int tile_tokens;        /* decode: tokens one workgroup iteration of the tuned kernel covers
+                               (0: generic kernel); attention: 0 */
 } kvq_plan_info;
 
 /* The plan of kv_int8_split_launch / kv_int8_simple_launch for these

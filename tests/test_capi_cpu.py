@@ -450,6 +450,9 @@ def test_decode_plan_kernels(L):
         return kvq.decode_plan(p)
 
     assert plan(8, 32, 32, 128, 4096).kernel == kvq.KERNEL_DECODE_VALU           # cfg1
+    assert plan(8, 32, 32, 128, 4096).tile_tokens == 128                          # 8 waves x 16 tokens
+    assert plan(1, 8, 8, 64, 1024).tile_tokens == 256 and plan(1, 8, 8, 64, 1024).splits == 1  # cfg0
+    assert plan(1, 32, 8, 128, 4096).tile_tokens == 128                           # matrix-core tiles
     i = plan(16, 32, 8, 128, 8192, lengths=A)                                    # cfg2
     assert (i.kernel, i.heads_per_group, i.split_plan) == (kvq.KERNEL_DECODE_MFMA, 4, kvq.SPLITS_TILES)
     i = plan(1, 32, 8, 128, 131072)                                              # cfg3
