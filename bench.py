@@ -323,6 +323,7 @@ class ConfigRun:
                          f"{' +append' if base.k_new is not None else ''}")
         self.settle_steps = 0
         self.rounds_ms = []
+        self.rounds_first = []  # this configuration's launch count at each timed round's start
         self.i = 0
         torch.cuda.synchronize()
 
@@ -348,12 +349,14 @@ class ConfigRun:
         torch = self.torch
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        first = self.i
         e0.record(stream)
         self.launch(self.steps, stream.cuda_stream)
         e1.record(stream)
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / self.steps
         self.rounds_ms.append(ms)
+        self.rounds_first.append(first)
         return ms
 
     def extras(self, stream):
@@ -397,7 +400,11 @@ class ConfigRun:
                        "us_per_step": [round(x * 1e3, 3) for x in self.rounds_ms],
                        "median": round(ms * 1e3, 3),
                        "min": round(min(self.rounds_ms) * 1e3, 3),
-                       "max": round(max(self.rounds_ms) * 1e3, 3)},
+                       "max": round(max(self.rounds_ms) * 1e3, 3),
+                       # Launch indices of this configuration's kernel (counting from its first
+                       # warm-up launch) at which each timed round starts: a kernel trace of the
+                       # same run selects the timed launches with them.
+                       "first_launch": list(self.rounds_first)},
             "settle_steps": self.settle_steps,
             "replicas": self.R,
             "kernel_us_isolated": round(kern_ms * 1e3, 3),
