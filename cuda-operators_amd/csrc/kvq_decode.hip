@@ -124,6 +124,7 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
     __shared__ float s_acc[kFastWaves][SG][D];
     __shared__ __align__(16) int s_newq[2][D / 4];  // appended K and V rows, packed int8
     __shared__ int s_last;
+    __shared__ MergeScratch s_merge;
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -381,7 +382,7 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
         }
         store_result(a, map, bhq0, h, dim, split, nsplit, M, L, A);
     }
-    finish_split(a, unit, map, bhq0, SG, nsplit, &s_last);
+    finish_split(a, unit, map, bhq0, SG, nsplit, &s_last, s_merge);
 }
 
 // Log-sum-exp merge of one element over nsplit records, 8 splits' (m, l, acc)

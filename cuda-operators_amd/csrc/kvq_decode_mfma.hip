@@ -105,11 +105,13 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
     // V tile buffers during the tile loop; the waves' results afterwards
     // (rows padded by one float, so the lanes of one result column, 16 rows
     // apart, hit different banks).
-    // (Before the tile loop, the in-kernel schedule's scratch.)
+    // (Before the tile loop, the in-kernel schedule's scratch; at the end, the
+    // merge's.)
     union TileOrResult {
         int8_t v[kMWaves][2][kMTile * D];
         float acc[kMWaves][16][D + 1];
         LptScratch lpt;
+        MergeScratch merge;  // finish_split, after s_acc's last read
     };
     static_assert(kMWaves * kWave == kLptThreads, "locate_lpt's workgroup size");
     __shared__ __align__(16) TileOrResult s_u;
@@ -536,7 +538,7 @@ __global__ __launch_bounds__(kMWaves* kWave) __attribute__((amdgpu_waves_per_eu(
         }
         store_result(a, map, bhq0, h, dim, split, nsplit, M, L, A);
     }
-    finish_split<true>(a, unit, map, bhq0, G, nsplit, &s_last);
+    finish_split<true>(a, unit, map, bhq0, G, nsplit, &s_last, s_u.merge);
 }
 
 

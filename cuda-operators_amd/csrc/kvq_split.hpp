@@ -454,14 +454,22 @@ __device__ inline bool merge_group_fits(const DecodeArgs& a, const RecMap& map, 
            nheads * nsplit <= kMergePairsPerThread * static_cast<int>(blockDim.x);
 }
 
-__device__ inline void merge_group(const DecodeArgs& a, const RecMap& map, size_t bhq0, int nheads, int nsplit) {
-    __shared__ float s_w[kMergeHeads][kMergeSplits];  // m, then the weights
-    __shared__ float s_L[kMergeHeads];
-    union LOrPart {
+// merge_group's LDS, provided by the kernel (which may overlay it on LDS it is
+// done with by the time finish_split's first barrier has passed).
+struct MergeScratch {
+    float w[kMergeHeads][kMergeSplits];  // m, then the weights
+    float L[kMergeHeads];
+    union {
         float l[kMergeHeads][kMergeSplits];  // phases 1-2
         float4 part[kMergeMaxThreads];       // phase 3
-    };
-    __shared__ LOrPart s_x;
+    } x;
+};
+
+__device__ inline void merge_group(const DecodeArgs& a, const RecMap& map, size_t bhq0, int nheads, int nsplit,
+                                   MergeScratch& ms) {
+    auto& s_w = ms.w;
+    auto& s_L = ms.L;
+    auto& s_x = ms.x;
     const int T = blockDim.x;
     const int t = threadIdx.x;
     const int lane = t & (kWave - 1);
@@ -668,13 +676,14 @@ __device__ inline void merge_flat_pairs(const DecodeArgs& a, const RecMap& map, 
 
 // Called by every thread of a workgroup after its store_result calls: counts
 // the split's arrival and, in the last workgroup of the work unit, merges the
-// records of rows [bhq0, bhq0 + nheads).  s_last: one int of LDS.  FLAT: up
+// records of rows [bhq0, bhq0 + nheads).  s_last: one int of LDS; ms: LDS
+// that nothing reads or writes after finish_split's first barrier.  FLAT: up
 // to kFlatSplits splits merge with merge_flat, up to twice that with
 // merge_flat_pairs (their registers are not worth taking from the FMA
 // kernel, whose ragged batches rarely split).
 template <bool FLAT = false>
 __device__ __forceinline__ void finish_split(const DecodeArgs& a, int unit, const RecMap& map, size_t bhq0,
-                                             int nheads, int nsplit, int* s_last) {
+                                             int nheads, int nsplit, int* s_last, MergeScratch& ms) {
     if (nsplit <= 1 || a.counters == nullptr) return;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's record stores have completed
     __syncthreads();
@@ -689,7 +698,7 @@ __device__ __forceinline__ void finish_split(const DecodeArgs& a, int unit, cons
         } else if (FLAT && nsplit <= 2 * kFlatSplits && merge_group_fits(a, map, nheads, nsplit)) {
             merge_flat_pairs(a, map, bhq0, nheads, nsplit);
         } else if (merge_group_fits(a, map, nheads, nsplit)) {
-            merge_group(a, map, bhq0, nheads, nsplit);
+            merge_group(a, map, bhq0, nheads, nsplit, ms);
         } else {
             for (int i = threadIdx.x; i < nheads * a.d; i += blockDim.x) {
                 const int h = i / a.d;
