@@ -367,6 +367,32 @@ def quantize_rows(x, q=None, scale=None, stream=None):
 # ---------------------------------------------------------------------------
 # paged cache
 # ---------------------------------------------------------------------------
+def check_paged(q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, lengths, out, k_new=None,
+                v_new=None) -> None:
+    """Dtype, shape, layout and device checks of a paged decode's tensors (the
+    C ABI sees only pointers and sizes, so a wrong dtype would read out of bounds)."""
+    B, Hq, d = q.shape
+    P_, Hkv, page, d2 = k_pages.shape
+    if d2 != d or Hq % Hkv:
+        raise ValueError("shape mismatch")
+    _need(q, torch.float32, (B, Hq, d), "q")
+    for t, n in ((k_pages, "k_pages"), (v_pages, "v_pages")):
+        _need(t, torch.int8, (P_, Hkv, page, d), n)
+    for t, n in ((k_scale_pages, "k_scale_pages"), (v_scale_pages, "v_scale_pages")):
+        _need(t, torch.float32, (P_, Hkv, page), n)
+    if block_table.dim() != 2 or block_table.shape[0] != B:
+        raise ValueError("block_table: want [B, max_pages_per_seq]")
+    _need(block_table, torch.int32, tuple(block_table.shape), "block_table")
+    if lengths is not None:
+        _need(lengths, torch.int32, (B,), "lengths")
+    _need(out, torch.float32, (B, Hq, d), "out")
+    if (k_new is None) != (v_new is None):
+        raise ValueError("k_new and v_new must be given together")
+    if k_new is not None:
+        _need(k_new, torch.float32, (B, Hkv, d), "k_new")
+        _need(v_new, torch.float32, (B, Hkv, d), "v_new")
+
+
 class PagedDecoder:
     """Decode over a paged cache (include/kvq.h part 3) with its own workspace.
 
@@ -376,24 +402,9 @@ class PagedDecoder:
 
     def __init__(self, q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, lengths, out,
                  max_seq_len=0, softmax_scale=0.0, num_splits=0, k_new=None, v_new=None, stream=None):
+        check_paged(q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, lengths, out, k_new, v_new)
         B, Hq, d = q.shape
-        P_, Hkv, page, d2 = k_pages.shape
-        if d2 != d or Hq % Hkv:
-            raise ValueError("shape mismatch")
-        _need(q, torch.float32, (B, Hq, d), "q")
-        for t, n in ((k_pages, "k_pages"), (v_pages, "v_pages")):
-            _need(t, torch.int8, (P_, Hkv, page, d), n)
-        for t, n in ((k_scale_pages, "k_scale_pages"), (v_scale_pages, "v_scale_pages")):
-            _need(t, torch.float32, (P_, Hkv, page), n)
-        if block_table.dim() != 2 or block_table.shape[0] != B:
-            raise ValueError("block_table: want [B, max_pages_per_seq]")
-        _need(block_table, torch.int32, tuple(block_table.shape), "block_table")
-        if lengths is not None:
-            _need(lengths, torch.int32, (B,), "lengths")
-        _need(out, torch.float32, (B, Hq, d), "out")
-        if k_new is not None:
-            _need(k_new, torch.float32, (B, Hkv, d), "k_new")
-            _need(v_new, torch.float32, (B, Hkv, d), "v_new")
+        P_, Hkv, page, _ = k_pages.shape
         self.keep = (q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, lengths, out, k_new, v_new)
         self.params = PagedDecodeParams(B, Hq, Hkv, d, page, P_, int(block_table.shape[1]), int(max_seq_len),
                                         _ptr(block_table), _ptr(lengths), _ptr(q), _ptr(k_pages), _ptr(v_pages),

@@ -32,7 +32,9 @@ workspace when it is large enough; otherwise the capture allocates one of its
 own, whose zero-fill is recorded in the graph and runs only when the graph is
 replayed, so that workspace belongs to that graph alone: it is never cached
 for eager calls (which could run before the first replay) nor for other
-captures.
+captures.  Graphs captured on one stream that share its cached workspace must
+not be replayed concurrently (on different streams), as for any two launches
+that share a workspace.
 """
 from __future__ import annotations
 
@@ -128,6 +130,7 @@ def paged_decode(q: Tensor, k_pages: Tensor, v_pages: Tensor, k_scale_pages: Ten
                  block_table: Tensor, lengths: Optional[Tensor], max_seq_len: int, softmax_scale: float,
                  num_splits: int, k_new: Optional[Tensor], v_new: Optional[Tensor]) -> Tensor:
     out = torch.empty_like(q)
+    kvq.check_paged(q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, lengths, out, k_new, v_new)
     B, Hq, d = q.shape
     P_, Hkv, page, _ = k_pages.shape
     p = kvq.PagedDecodeParams(B, Hq, Hkv, d, page, P_, int(block_table.shape[1]), int(max_seq_len),

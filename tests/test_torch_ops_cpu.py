@@ -39,3 +39,19 @@ def test_fake_shapes():
         qa, ka = torch.empty(300, 64), torch.empty(1000, 64)
         out = torch.ops.kvq.attention(qa, ka, ka, 0.0, 0)
         assert out.shape == qa.shape and out.dtype == torch.float32
+
+
+def test_paged_decode_checks_tensors_before_launch():
+    """The paged operator checks dtypes, shapes and devices like the contiguous
+    one: the C ABI sees only pointers, so these would otherwise read out of bounds."""
+    import pytest
+    kvq = importlib.import_module("cuda-operators_amd.kvq")
+    B, Hq, Hkv, d = 2, 8, 2, 64
+    q = torch.empty(B, Hq, d)
+    pages = torch.empty(6, Hkv, 16, d, dtype=torch.int8)
+    ps = torch.empty(6, Hkv, 16)
+    table = torch.zeros(B, 3, dtype=torch.int32)
+    with pytest.raises(ValueError, match="q: want contiguous cuda"):
+        torch.ops.kvq.paged_decode(q, pages, pages, ps, ps, table, None, 48, 0.0, 0, None, None)
+    with pytest.raises(ValueError, match="shape mismatch"):
+        kvq.check_paged(q, pages[..., :32], pages, ps, ps, table, None, q)
