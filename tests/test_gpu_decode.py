@@ -122,6 +122,26 @@ def test_merge_of_17_to_32_splits(o, splits, L):
     assert_close(got, want, what=f"splits={splits} L={L}")
 
 
+@pytest.mark.parametrize("splits", [33, 48, 100, 257])
+def test_merge_past_32_splits(o, splits):
+    """More than 32 splits: the last split's workgroup merges with the
+    two-phase group merge ((m, l) pairs into LDS, then the accumulators, 16
+    in flight per thread), every sequence length split differently; 257
+    splits is past that merge's limit of 256 and takes the per-element merge."""
+    L = splits * 128 - 28
+    rng = np.random.default_rng(splits)
+    lengths = np.array([L, 1, L - 1, (2 * L) // 5], np.int32)
+    p = make_problem(rng, 4, 8, 2, L, 128, o.quantize_rows, dist="outlier", lengths=lengths)
+    prm = kvq.DecodeParams(batch=4, num_q_heads=8, num_kv_heads=2, head_dim=128, capacity=L, max_seq_len=L,
+                           lengths=4096, q=4096, k_cache=4096, v_cache=4096, k_scale=4096, v_scale=4096,
+                           out=4096, num_splits=splits)
+    info = kvq.decode_plan(prm)
+    assert info.kernel == kvq.KERNEL_DECODE_MFMA and info.splits > 32, (info.kernel, info.splits)
+    got = _gpu.decode(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths, splits=splits)[0]
+    want = o.decode_f32(p["q"], p["k"], p["v"], p["ks"], p["vs"], lengths=lengths)
+    assert_close(got, want, what=f"splits={splits} L={L}")
+
+
 @pytest.mark.parametrize("G", [1, 2, 3, 4, 6, 8, 12, 16])
 @pytest.mark.parametrize("d", [64, 128])
 def test_group_sizes(o, G, d):
