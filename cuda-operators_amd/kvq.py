@@ -102,6 +102,7 @@ class AttentionParams(ctypes.Structure):
         ("softmax_scale", ctypes.c_float), ("num_splits", _int),
     ]
 
+
 class PlanInfo(ctypes.Structure):
     """struct kvq_plan_info (include/kvq.h part 6)."""
     _fields_ = [
@@ -238,15 +239,31 @@ def _need(t, dtype, shape, name):
 # ---------------------------------------------------------------------------
 # reference ABI
 # ---------------------------------------------------------------------------
+def _check_reference(Q, K, V, k_scale, v_scale, out):
+    """Dtypes, shapes and devices of a reference-ABI call (the C entry points
+    see only pointers and (H, N, d)); returns (H, N, d)."""
+    H, N, d = K.shape
+    _need(Q, torch.float32, (H, d), "Q")
+    _need(K, torch.int8, (H, N, d), "K")
+    _need(V, torch.int8, (H, N, d), "V")
+    _need(k_scale, torch.float32, (H, N), "k_scale")
+    _need(v_scale, torch.float32, (H, N), "v_scale")
+    _need(out, torch.float32, (H, d), "out")
+    return H, N, d
+
+
 def solve(Q, K, V, k_scale, v_scale, out) -> None:
     """Legacy `solve` on the null stream: Q[H,d], K/V[H,N,d] int8, scales[H,N], out[H,d]."""
-    H, N, d = K.shape
+    H, N, d = _check_reference(Q, K, V, k_scale, v_scale, out)
     lib().solve(_ptr(Q), _ptr(K), _ptr(V), _ptr(k_scale), _ptr(v_scale), _ptr(out), H, N, d)
 
 
 def kv_int8_split_launch(Q, K, V, k_scale, v_scale, out, S, stream=None, simple=False) -> int:
     """Stream-aware reference launch; S is H*N floats of caller scratch. Returns the hipError code."""
-    H, N, d = K.shape
+    H, N, d = _check_reference(Q, K, V, k_scale, v_scale, out)
+    if not (isinstance(S, torch.Tensor) and S.dtype == torch.float32 and S.is_contiguous()
+            and S.device.type == "cuda" and S.numel() >= H * N):
+        raise ValueError(f"S: want contiguous cuda float32 scratch of at least {H * N} elements")
     fn = lib().kv_int8_simple_launch if simple else lib().kv_int8_split_launch
     return int(fn(_ptr(Q), _ptr(K), _ptr(V), _ptr(k_scale), _ptr(v_scale), _ptr(out), H, N, d, _ptr(S),
                   _stream(stream)))
@@ -343,9 +360,29 @@ def decode(q, k_cache, v_cache, k_scale, v_scale, lengths=None, max_seq_len=0, s
     return out
 
 
+def _check_cache(k_cache, v_cache, k_scale, v_scale, what="cache"):
+    """An int8 K/V pair [X, Hkv, T, d] with fp32 scales [X, Hkv, T] (X: batch
+    or pages, T: capacity or page size); returns (X, Hkv, T, d)."""
+    X, Hkv, T, d = k_cache.shape
+    for t, n in ((k_cache, f"k_{what}"), (v_cache, f"v_{what}")):
+        _need(t, torch.int8, (X, Hkv, T, d), n)
+    for t, n in ((k_scale, "k_scale"), (v_scale, "v_scale")):
+        _need(t, torch.float32, (X, Hkv, T), n)
+    return X, Hkv, T, d
+
+
+def _check_new_rows(k_new, v_new, B, Hkv, d):
+    for t, n in ((k_new, "k_new"), (v_new, "v_new")):
+        _need(t, torch.float32, (B, Hkv, d), n)
+
+
 def append(k_new, v_new, k_cache, v_cache, k_scale, v_scale, positions=None, uniform_position=0,
            stream=None) -> None:
-    B, Hkv, cap, d = k_cache.shape
+    """One new K/V token per (b, kv head) into the contiguous cache (kvq_append_launch)."""
+    B, Hkv, cap, d = _check_cache(k_cache, v_cache, k_scale, v_scale)
+    _check_new_rows(k_new, v_new, B, Hkv, d)
+    if positions is not None:
+        _need(positions, torch.int32, (B,), "positions")
     p = AppendParams(B, Hkv, d, cap, _ptr(positions), int(uniform_position), _ptr(k_new), _ptr(v_new),
                      _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale))
     _check("kvq_append_launch", lib().kvq_append_launch(ctypes.byref(p), _stream(stream)))
@@ -355,10 +392,13 @@ def quantize_rows(x, q=None, scale=None, stream=None):
     """x[..., d] fp32 cuda -> (q int8 [..., d], scale fp32 [...])."""
     d = x.shape[-1]
     rows = x.numel() // d if d else 0
+    _need(x, torch.float32, tuple(x.shape), "x")
     if q is None:
         q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
     if scale is None:
         scale = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    _need(q, torch.int8, tuple(x.shape), "q")
+    _need(scale, torch.float32, tuple(x.shape[:-1]), "scale")
     _check("kvq_quantize_rows_launch",
            lib().kvq_quantize_rows_launch(_ptr(x), rows, d, _ptr(q), _ptr(scale), _stream(stream)))
     return q, scale
@@ -426,8 +466,14 @@ class PagedDecoder:
 def paged_append(k_new, v_new, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, positions=None,
                  uniform_position=0, stream=None) -> None:
     """One new K/V token per (b, kv head) into its page slot (kvq_paged_append_launch)."""
-    P_, Hkv, page, d = k_pages.shape
+    P_, Hkv, page, d = _check_cache(k_pages, v_pages, k_scale_pages, v_scale_pages, "pages")
+    if block_table.dim() != 2:
+        raise ValueError("block_table: want [B, max_pages_per_seq]")
     B = block_table.shape[0]
+    _need(block_table, torch.int32, tuple(block_table.shape), "block_table")
+    _check_new_rows(k_new, v_new, B, Hkv, d)
+    if positions is not None:
+        _need(positions, torch.int32, (B,), "positions")
     p = PagedAppendParams(B, Hkv, d, page, P_, int(block_table.shape[1]), _ptr(block_table), _ptr(positions),
                           int(uniform_position), _ptr(k_new), _ptr(v_new), _ptr(k_pages), _ptr(v_pages),
                           _ptr(k_scale_pages), _ptr(v_scale_pages))
@@ -450,12 +496,22 @@ def prefill(k_new, v_new, k_cache, v_cache, k_scale, v_scale, start=None, unifor
         raise TypeError("k_new must be float32 or bfloat16")
     for t, n in ((k_new, "k_new"), (v_new, "v_new")):
         _need(t, k_new.dtype, (B, Hkv, L, d), n)
+    X, Hkv2, T, d2 = _check_cache(k_cache, v_cache, k_scale, v_scale)
+    if (Hkv2, d2) != (Hkv, d):
+        raise ValueError("shape mismatch")
+    if start is not None:
+        _need(start, torch.int32, (B,), "start")
     if block_table is None:
-        cap = k_cache.shape[2]
+        if X != B:
+            raise ValueError("shape mismatch")
+        cap = T
         pg = (0, 0, 0)
     else:
+        if block_table.dim() != 2 or block_table.shape[0] != B:
+            raise ValueError("block_table: want [B, max_pages_per_seq]")
+        _need(block_table, torch.int32, tuple(block_table.shape), "block_table")
         cap = 0
-        pg = (k_cache.shape[2], k_cache.shape[0], int(block_table.shape[1]))
+        pg = (T, X, int(block_table.shape[1]))
     p = PrefillParams(B, Hkv, d, L, dt, _ptr(k_new), _ptr(v_new), _ptr(start), int(uniform_start), cap,
                       _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale), _ptr(block_table), *pg)
     _check("kvq_prefill_quantize_launch", lib().kvq_prefill_quantize_launch(ctypes.byref(p), _stream(stream)))

@@ -535,3 +535,35 @@ def test_attention_compat_library_exports_solve():
     assert "attention_online_launch" in und
     A = kvq.attention_lib()
     assert A.solve is not kvq.lib().solve
+
+
+def test_python_reference_wrappers_check_tensors():
+    """kvq.solve / kvq.kv_int8_split_launch check dtypes, shapes and devices
+    before calling the C ABI, which sees only pointers and (H, N, d)."""
+    import torch
+    H, N, d = 2, 16, 64
+    Q = torch.zeros(H, d)
+    K = torch.zeros(H, N, d, dtype=torch.int8)
+    s = torch.zeros(H, N)
+    with pytest.raises(ValueError, match="Q: want contiguous cuda"):
+        kvq.solve(Q, K, K, s, s, Q)
+    with pytest.raises(ValueError, match="Q: want contiguous cuda"):
+        kvq.kv_int8_split_launch(Q, K, K, s, s, Q, torch.zeros(H * N))
+
+
+def test_python_cache_wrappers_check_tensors():
+    """append / paged_append / prefill / quantize_rows check their tensors
+    before the C ABI (which would read a wrong dtype out of bounds)."""
+    import torch
+    B, Hkv, cap, d = 2, 2, 8, 64
+    k = torch.zeros(B, Hkv, cap, d, dtype=torch.int8)
+    s = torch.zeros(B, Hkv, cap)
+    x = torch.zeros(B, Hkv, d)
+    with pytest.raises(ValueError, match="k_cache: want contiguous cuda"):
+        kvq.append(x, x, k, k, s, s)
+    with pytest.raises(ValueError, match="k_pages: want contiguous cuda"):
+        kvq.paged_append(x, x, k, k, s, s, torch.zeros(B, 1, dtype=torch.int32))
+    with pytest.raises(ValueError, match="k_new: want contiguous cuda"):
+        kvq.prefill(torch.zeros(B, Hkv, 3, d), torch.zeros(B, Hkv, 3, d), k, k, s, s)
+    with pytest.raises(ValueError, match="x: want contiguous cuda"):
+        kvq.quantize_rows(x)
