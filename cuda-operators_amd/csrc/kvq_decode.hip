@@ -38,6 +38,9 @@
 namespace kvq {
 namespace {
 
+// Ranges of at least this many workgroup blocks give their last block to the
+// first wave of each SIMD (see the tile loop of decode_fast).
+constexpr int kRebalanceBlocks = 8;
 #ifndef KVQ_FAST_WAVES
 #define KVQ_FAST_WAVES 8
 #endif
@@ -257,8 +260,7 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
         else return 0;
     };
     int pg_next = page_entry(base);
-    auto next_row = [&](int nb) -> size_t {  // row of the tile at nb - BSTEP; prefetch nb's entry
-        const int tb = nb - Geo::BSTEP;
+    auto row_of = [&](int tb, int nb) -> size_t {  // row of the tile at tb; prefetch the entry of nb
         if constexpr (PAGED) {
             const int page = min(max(__builtin_amdgcn_readfirstlane(pg_next), 0), a.pages.num_pages - 1);
             pg_next = page_entry(nb);
@@ -267,11 +269,37 @@ __global__ __launch_bounds__(kFastWaves* kWave) void decode_fast(const DecodeArg
             return row0 + tb;
         }
     };
+    auto next_row = [&](int nb) -> size_t { return row_of(nb - Geo::BSTEP, nb); };
     if constexpr (!Geo::PIPE) {
-        for (; base < tend; base += Geo::BSTEP) {
+        // The two waves that share a SIMD do not stream at the same rate: the
+        // first one dispatched (waves 0 .. kFastWaves/2 - 1) wins issue
+        // arbitration and ends its tile loop ~1.6 us before its partner at
+        // cfg1.  In ranges of kRebalanceBlocks blocks or more, the last block
+        // therefore goes to the first waves alone, two steps each (a fixed
+        // assignment: outputs stay bit-reproducible); shorter ranges keep
+        // every wave busy instead.  Measured and applied at SG = 1 only (at
+        // SG = 2 the extra code took some instantiations past 128 VGPRs).
+        const int nblk = (tend - t0 + Geo::BSTEP - 1) / Geo::BSTEP;
+        const int lastb = SG == 1 && nblk >= kRebalanceBlocks ? t0 + (nblk - 1) * Geo::BSTEP : tend;
+        for (; base < lastb; base += Geo::BSTEP) {
             Tile tt;
             load_tile(tt, base, next_row(base + Geo::BSTEP));
             run_tile(tt, base);
+        }
+        const int wvu = __builtin_amdgcn_readfirstlane(wave);
+        if (lastb < tend && wvu < kFastWaves / 2) {
+            // base == lastb + wvu * WSTEP, whose page entry the loop prefetched
+            const int b1 = base + (kFastWaves / 2) * Geo::WSTEP;
+            if (base < tend) {
+                Tile tt;
+                load_tile(tt, base, row_of(base, b1));
+                run_tile(tt, base);
+            }
+            if (b1 < tend) {
+                Tile tt;
+                load_tile(tt, b1, row_of(b1, b1 + Geo::BSTEP));
+                run_tile(tt, b1);
+            }
         }
     } else {
         Tile ta, tb;
