@@ -94,6 +94,10 @@ def parse():
                     help="also run a plain 1 GiB copy kernel (PMC byte-counter calibration)")
     ap.add_argument("--traffic", default=os.path.join(REPO, "profiles", "traffic.json"),
                     help="measured HBM traffic summary (from rocprofv3 --pmc), if present")
+    ap.add_argument("--placement", type=int, default=0,
+                    help="instead of the bench line: N separately allocated caches of --config, each timed "
+                         "alone (contiguous layout), to show how the step time depends on where a cache sits")
+    ap.add_argument("--placement-steps", type=int, default=200, help="timed steps per cache in --placement")
     return ap.parse_args()
 
 
@@ -475,6 +479,36 @@ def verify_line(line):
     return bad
 
 
+def placement_sweep(args, torch, kvq, synth, stream):
+    """--placement N: N caches of one configuration, allocated one after
+    another; --warmup steps over all of them (steady clocks), then each cache
+    launched 20 times untimed and --placement-steps times between two events,
+    alone.  Prints one JSON line with each cache's K and V addresses and its
+    us/step."""
+    a = argparse.Namespace(**vars(args))
+    a.replicas = args.placement
+    run = ConfigRun(a, torch, kvq, synth, args.config, args.placement_steps)
+    sh = stream.cuda_stream
+    run.launch(args.warmup, sh)
+    torch.cuda.synchronize()
+    caches = []
+    for r, dec in enumerate(run.decs):
+        for _ in range(20):
+            dec(sh)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.placement_steps):
+            dec(sh)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        k, v = dec.keep[1], dec.keep[2]
+        caches.append({"cache": r, "k": hex(k.data_ptr()), "v": hex(v.data_ptr()),
+                       "us_per_step": round(e0.elapsed_time(e1) * 1e3 / args.placement_steps, 3)})
+    print(json.dumps({"mode": "placement", "workload": run.workload, "kernel": run.kernel,
+                      "steps_per_cache": args.placement_steps, "caches": caches}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -492,6 +526,9 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
+    if args.placement > 0:
+        placement_sweep(args, torch, kvq, synth, stream)
+        return
 
     # Every configuration is set up first (seeded problems and replicas, about
     # 10 GB in all), then timed in rounds: round r runs them in rotated order,
