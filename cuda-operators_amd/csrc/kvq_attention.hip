@@ -489,8 +489,8 @@ __global__ __launch_bounds__(W* KW* kWave) void attention_direct(const AttnArgs 
 // a group of L lanes, each with E = D/L of its dims: float4 number j·L + lane
 // of the row, for j < E/4, so each load instruction reads 16·L contiguous
 // bytes per group.  A wave covers 64/L keys per load and keeps 4 loads of K
-// and 4 of V in flight per lane (8 KB per wave at any D), so a workgroup step
-// is 4096/D keys whatever L is.  Each key group keeps its own online-softmax
+// and 4 of V in flight per lane (8 KB per wave at any D), so a wave step is
+// 1024/D keys whatever L is.  Each key group keeps its own online-softmax
 // state per query; its scores are sums over the group's lanes (DPP within a
 // 16-lane row, ds_bpermute across rows).  L = D/4 (4 dims per lane), except
 // D/8 (8 dims per lane) at d >= 128 with 4-8 queries: there the per-key
@@ -500,22 +500,30 @@ __global__ __launch_bounds__(W* KW* kWave) void attention_direct(const AttnArgs 
 // The epilogue merges the groups of a wave (shuffles), then the waves
 // (LDS), and writes the output, or the split's (m, l, acc) record for
 // attention_merge.
+// Waves per workgroup: 4 (one per SIMD; about 32 KB of K/V in flight per
+// CU, the streaming optimum), or 8 for one query over short splits, where two
+// waves per SIMD hide more of each split's start (M = 1, N = 65536: d = 128
+// 13.52 against 13.74 us, d = 64 8.63 against 9.10 us; at 1024 keys per split
+// and more 8 waves ran slower, N = 2^20: 157.2 against 151.9 us, and at 32-64
+// keys per split no faster).
 constexpr int kRowsWaves = 4;
+constexpr int kRowsWavesShort = 8;
+constexpr int kRowsShortMin = 128, kRowsShortMax = 512;  // keys per split that take kRowsWavesShort waves (one query)
 constexpr int kRowsLoads = 4;  // float4 loads of K (and of V) in flight per lane
 constexpr int kRowsMaxQueries = kAttnRowsBlock;
-template <int D, int QM>
+template <int D, int QM, int W = kRowsWaves>
 struct RowsShape {
     static constexpr int L = QM >= 4 && D >= 128 ? D / 8 : D / 4;  // lanes per key row
     static constexpr int E = D / L;                              // dims per lane
     static constexpr int NV = E / 4;                             // float4 loads per row per lane
     static constexpr int U = kRowsLoads / NV;                    // keys per lane per step
     static constexpr int KW = kWave / L;                         // keys per wave load
-    static constexpr int T = kRowsWaves * KW * U;                // keys per workgroup step
-    static_assert(T == 4096 / D, "a workgroup step is 4096/D keys at any group width");
+    static constexpr int T = W * KW * U;                         // keys per workgroup step
+    static_assert(T == W * 1024 / D, "a wave step is 1024/D keys at any group width");
 };
-template <int D>
+template <int D, int QM>
 constexpr int rows_tile() {
-    return RowsShape<D, 1>::T;
+    return RowsShape<D, QM>::T;  // the 4-wave step, which sizes the splits
 }
 
 template <int L>
@@ -537,9 +545,9 @@ __device__ __forceinline__ float4 load_row16(const float* p) {
     return make_float4(t.x, t.y, t.z, t.w);
 }
 
-template <int D, int QM>
-__global__ __launch_bounds__(kRowsWaves* kWave) void attention_rows(const AttnArgs a) {
-    using S = RowsShape<D, QM>;
+template <int D, int QM, int W>
+__global__ __launch_bounds__(W* kWave) void attention_rows(const AttnArgs a) {
+    using S = RowsShape<D, QM, W>;
     constexpr int L = S::L, E = S::E, NV = S::NV, U = S::U, KW = S::KW, T = S::T;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -635,8 +643,8 @@ __global__ __launch_bounds__(kRowsWaves* kWave) void attention_rows(const AttnAr
     }
 
     // The workgroup's waves, through LDS (float4 column c4 = jL + ds).
-    __shared__ float2 s_ml[kRowsWaves][QM];
-    __shared__ float4 s_acc[kRowsWaves][QM][D / 4];
+    __shared__ float2 s_ml[W][QM];
+    __shared__ float4 s_acc[W][QM][D / 4];
     if (kg == 0) {
 #pragma unroll
         for (int qi = 0; qi < QM; qi++) {
@@ -648,18 +656,18 @@ __global__ __launch_bounds__(kRowsWaves* kWave) void attention_rows(const AttnAr
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < QM * (D / 4); i += kRowsWaves * kWave) {
+    for (int i = threadIdx.x; i < QM * (D / 4); i += W * kWave) {
         const int qi = i / (D / 4);
         const int c4 = i - qi * (D / 4);
         const int q = q0 + qi;
         if (q >= a.M) continue;
         float mm = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kRowsWaves; w++) mm = fmaxf(mm, s_ml[w][qi].x);
+        for (int w = 0; w < W; w++) mm = fmaxf(mm, s_ml[w][qi].x);
         float ls = 0.0f;
         float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-        for (int w = 0; w < kRowsWaves; w++) {
+        for (int w = 0; w < W; w++) {
             const float2 ml = s_ml[w][qi];
             const float c = ml.x == -INFINITY ? 0.0f : fast_exp2(ml.x - mm);
             const float4 x = s_acc[w][qi][c4];
@@ -738,12 +746,21 @@ int attention_rows_queries(int M) {
     if (M <= 4) return 4;
     return M <= kRowsMaxQueries ? kRowsMaxQueries : 0;
 }
-int attention_rows_tile(int d) {
+template <int D>
+int rows_tile_d(int qm) {
+    switch (qm) {
+        case 1: return rows_tile<D, 1>();
+        case 2: return rows_tile<D, 2>();
+        case 4: return rows_tile<D, 4>();
+        default: return rows_tile<D, kRowsMaxQueries>();
+    }
+}
+int attention_rows_tile(int d, int qm) {
     switch (d) {
-        case 32: return rows_tile<32>();
-        case 64: return rows_tile<64>();
-        case 128: return rows_tile<128>();
-        default: return rows_tile<256>();
+        case 32: return rows_tile_d<32>(qm);
+        case 64: return rows_tile_d<64>(qm);
+        case 128: return rows_tile_d<128>(qm);
+        default: return rows_tile_d<256>(qm);
     }
 }
 
@@ -761,7 +778,10 @@ void launch_mfma_attention(const AttnArgs& a, int glog, hipStream_t stream) {
 template <int D, int QM>
 void launch_rows_attention(const AttnArgs& a, int glog, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((a.M + QM - 1) / QM), static_cast<unsigned>(a.splits));
-    hipLaunchKernelGGL((attention_rows<D, QM>), grid, dim3(kRowsWaves * kWave), 0, stream, a);
+    if (QM == 1 && a.chunk >= kRowsShortMin && a.chunk <= kRowsShortMax)
+        hipLaunchKernelGGL((attention_rows<D, QM, kRowsWavesShort>), grid, dim3(kRowsWavesShort * kWave), 0, stream, a);
+    else
+        hipLaunchKernelGGL((attention_rows<D, QM, kRowsWaves>), grid, dim3(kRowsWaves * kWave), 0, stream, a);
     if (a.splits > 1) {
         const dim3 mgrid(static_cast<unsigned>(
             ((static_cast<long long>(a.M) * (D / 4) << glog) + kMergeThreads - 1) / kMergeThreads));

@@ -697,7 +697,7 @@ AttnPlan attention_plan(int M, int N, int d, bool aligned, int requested) {
         // A few queries: the VALU kernel, query blocks of qm, key splits to
         // fill KVQ_ATTN_ROWS_TARGET(qm) workgroups per query block.
         p.qblock = qm;
-        const long long rt = kvq::attention_rows_tile(d);
+        const long long rt = kvq::attention_rows_tile(d, qm);
         const long long rtiles = (static_cast<long long>(N) + rt - 1) / rt;
         const long long want = std::max(1LL, std::min({requested > 0 ? static_cast<long long>(requested)
                                                                      : static_cast<long long>(KVQ_ATTN_ROWS_TARGET(qm)),

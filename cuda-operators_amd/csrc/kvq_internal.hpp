@@ -208,7 +208,7 @@ int attention_key_tile(int d);    // keys per LDS tile of the matrix-core kernel
 int attention_max_splits(int d);  // most key splits per matrix-core launch (tuned d)
 int attention_direct_dim(int d);  // attention_direct handles head dim d
 int attention_rows_queries(int M);  // queries per workgroup of the few-query kernel (0: M too large)
-int attention_rows_tile(int d);     // keys per workgroup step of the few-query kernel (tuned d)
+int attention_rows_tile(int d, int qm);  // keys per workgroup step of the few-query kernel (tuned d, qm queries)
 hipError_t launch_attention(const AttnArgs& a, hipStream_t stream);
 
 // Tokens one workgroup iteration of the fast kernel covers for head dim d and
