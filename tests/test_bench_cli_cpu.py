@@ -24,7 +24,7 @@ def test_bench_help_lists_options():
     assert r.returncode == 0
     for opt in ("--gpus", "--steps", "--warmup", "--settle-ms", "--config", "--splits", "--page-size",
                 "--page-order", "--seed", "--no-cpu", "--cpu-budget", "--configs", "--config-steps",
-                "--config-cpu-budget"):
+                "--config-cpu-budget", "--placement", "--placement-steps"):
         assert opt in r.stdout, opt
 
 
