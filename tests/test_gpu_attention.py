@@ -56,6 +56,25 @@ def test_attention_few_queries(o, d, M, N):
     _close(down(out), o.attention_f32(q, k, v), f"M={M} N={N} d={d}")
 
 
+@pytest.mark.parametrize("N,splits", [(32768, 0), (40001, 0), (131072, 0), (140000, 0), (65536, 128), (65536, 512),
+                                      (20000, 100)])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
+def test_attention_one_query_split_sizes(o, d, N, splits):
+    """One query: splits of 128-512 keys run 8 waves per workgroup, others 4
+    (the window's edges, a ragged last split, explicit split requests on
+    both sides of it)."""
+    rng = np.random.default_rng(N + d + splits)
+    q, k, v = _problem(rng, 1, N, d)
+    gq, gk, gv = up(q), up(k), up(v)
+    out = _gpu.poisoned((1, d))
+    p = kvq.attention_params(gq, gk, gv, out, num_splits=splits)
+    info = kvq.attention_plan(p)
+    assert info.kernel == kvq.KERNEL_ATTENTION_ROWS and info.query_block == 1, (info.kernel, info.query_block)
+    kvq.attention(gq, gk, gv, out, num_splits=splits)
+    torch.cuda.synchronize()
+    _close(down(out), o.attention_f32(q, k, v), f"N={N} d={d} splits={splits} chunk={info.chunk}")
+
+
 @pytest.mark.parametrize("splits", [1, 2, 5, 1 << 20])
 @pytest.mark.parametrize("M", [4, 6])
 @pytest.mark.parametrize("d", [64, 128, 256])
