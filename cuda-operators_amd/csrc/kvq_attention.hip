@@ -778,7 +778,9 @@ void launch_mfma_attention(const AttnArgs& a, int glog, hipStream_t stream) {
 template <int D, int QM>
 void launch_rows_attention(const AttnArgs& a, int glog, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((a.M + QM - 1) / QM), static_cast<unsigned>(a.splits));
-    if (QM == 1 && a.chunk >= kRowsShortMin && a.chunk <= kRowsShortMax)
+    // (and at least one 8-wave step per split, so no wave idles: d = 32 from 256 keys)
+    if (QM == 1 && a.chunk >= kRowsShortMin && a.chunk >= RowsShape<D, QM, kRowsWavesShort>::T &&
+        a.chunk <= kRowsShortMax)
         hipLaunchKernelGGL((attention_rows<D, QM, kRowsWavesShort>), grid, dim3(kRowsWavesShort * kWave), 0, stream, a);
     else
         hipLaunchKernelGGL((attention_rows<D, QM, kRowsWaves>), grid, dim3(kRowsWaves * kWave), 0, stream, a);
